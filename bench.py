@@ -1,0 +1,219 @@
+"""Benchmark of the NF4 frozen-weight path on one MI355X.
+
+Default workload (the shape the throughput targets are quoted at): a LoRA
+training step on an NF4 base, W [14336, 4096] (fp16 N(0, 0.02) source,
+blocksize 64, dequantized to bf16), X bf16 [8192, 4096] N(0, 1), LoRA rank 16
+(A, B bf16 N(0, 0.01), scale 1). One step = fused forward
+Y = X.W^T + X.A^T.B^T and fused backward dX = dY.W (+ LoRA), plus the LoRA
+weight gradients. ``value`` counts the two frozen-base GEMMs only
+(2 x 2.M.N.K = 1924.1 GFLOP per step); the LoRA flops are reported apart.
+
+Also measured, each with HIP events on the stream the kernels run on:
+  * the fused forward kernel alone (the roofline line, dense-bf16 MFMA bound);
+  * the NF4 dequantize kernel on the same W to bf16 (HBM bound, 2.5625 B/element);
+  * the unfused path the reference uses (dequantize + torch.matmul);
+  * the CPU oracle (C restatement, all host threads) on a bounded sample.
+
+    python bench.py [--steps K] [--warmup W] [--workload lora_step|layer_stream]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "NF4 dequant GB/s (% HBM peak); fused NF4-GEMM TFLOP/s (% MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def seeded(torch, shape, seed, std, dtype, device):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype).to(device)
+
+
+def event_time_ms(torch, fn, reps):
+    """Average duration of fn() over reps launches, timed with HIP events on the
+    current stream (where the library launches its kernels)."""
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(torch, w_half, N, K, sample_rows):
+    """Oracle on the host: C-restatement dequantize of the whole W (all threads),
+    then an fp32 torch matmul of `sample_rows` rows of X with it."""
+    import numpy as np
+
+    from oracle import c_oracle as C
+    from oracle import nf4_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    wbits = w_half.cpu().view(torch.int16).numpy().view(np.uint16)
+    packed, absmax = C.quantize(wbits, O.DT_F16, 64, "argmin", threads)
+    n = N * K
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        wd = C.dequantize(packed, absmax, n, 64, O.DT_BF16, threads)
+        reps += 1
+        if time.perf_counter() - t0 > 3.0:
+            break
+    deq_s = (time.perf_counter() - t0) / reps
+    w32 = torch.from_numpy(wd.view(np.int16).reshape(N, K)).view(torch.bfloat16).float()
+    x = torch.randn(sample_rows, K)
+    t0 = time.perf_counter()
+    y = x @ w32.t()
+    mm_s = time.perf_counter() - t0
+    del y
+    flops = 2.0 * sample_rows * N * K
+    return {
+        "value": round(flops / (deq_s + mm_s) / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle C dequantize of W [{N},{K}] to bf16 + fp32 torch matmul of {sample_rows} "
+                   f"rows of X (of 8192)"),
+        "dequant_gbs": round(2.5625 * n / deq_s / 1e9, 3),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_lora_step(args):
+    import torch
+
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit
+    from stratum_amd.nf4_linear import nf4_linear
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    N, K, M, R = 14336, 4096, 8192, 16
+    w = seeded(torch, (N, K), 0, 0.02, torch.float16, dev)
+    packed, state = quantize_4bit(w)
+    state.dtype = torch.bfloat16
+    absmax = state.absmax
+    x = seeded(torch, (M, K), 1, 1.0, torch.bfloat16, dev).requires_grad_(True)
+    A = seeded(torch, (R, K), 2, 0.01, torch.bfloat16, dev).requires_grad_(True)
+    B = seeded(torch, (N, R), 3, 0.01, torch.bfloat16, dev).requires_grad_(True)
+    dy = seeded(torch, (M, N), 4, 1.0, torch.bfloat16, dev)
+
+    def step():
+        y = nf4_linear(x, packed, state, None, A, B, 1.0)
+        y.backward(dy)
+        x.grad = None
+        A.grad = None
+        B.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+    base_flops = 2 * 2.0 * M * N * K
+    lora_flops = 2.0 * M * K * R + 2.0 * M * R * N           # forward rank-16 path
+    lora_flops += 2.0 * M * N * R + 2.0 * M * R * K          # dX rank-16 term
+    lora_flops += 2.0 * R * M * K + 2.0 * N * M * R          # dA, dB
+    value = base_flops / (elapsed / args.steps) / 1e12
+
+    xd = x.detach()
+    reps = max(5, args.kernel_reps)
+    fwd_ms = event_time_ms(torch, lambda: nf4_gemm_fwd(xd, packed, absmax, (N, K), 64), reps)
+    bwd_ms = event_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy, packed, absmax, (N, K), 64), reps)
+    gemm_flops = 2.0 * M * N * K
+    fwd_tf = gemm_flops / (fwd_ms * 1e-3) / 1e12
+    bwd_tf = gemm_flops / (bwd_ms * 1e-3) / 1e12
+
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    deq_ms = event_time_ms(torch, lambda: dequantize_4bit(packed, state, out=out), reps * 4)
+    deq_bytes = 2.5625 * N * K
+    deq_gbs = deq_bytes / (deq_ms * 1e-3) / 1e9
+
+    def unfused():
+        wt = dequantize_4bit(packed, state, out=out)
+        return xd @ wt.t()
+
+    unf_ms = event_time_ms(torch, unfused, reps)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) fp16 weight quantized to NF4, N(0,1) bf16 activations)",
+        "config": {"workload": "lora_step_nf4_w14336x4096_x8192", "M": M, "N": N, "K": K, "lora_rank": R,
+                   "blocksize": 64, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_fwd<BF16>", "achieved": round(fwd_tf, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
+        "bwd_dx": {"kernel": "k_gemm_bwd<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
+                   "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
+        "dequant": {"kernel": "k_dequantize<BF16>", "value": round(deq_gbs, 1), "unit": "GB/s",
+                    "frac": round(deq_gbs / HBM_PEAK_GBS, 4), "peak": HBM_PEAK_GBS,
+                    "avg_kernel_ms": round(deq_ms, 4), "bytes_per_launch": deq_bytes},
+        "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
+                        "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
+        "lora_gflop_per_step": round(lora_flops / 1e9, 2),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, w, N, K, args.cpu_rows)
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="lora_step", choices=["lora_step"])
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the NF4 path is sharded by weight rows with no collective on one GPU's share -- "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    line = run_lora_step(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,147 @@
+/*
+ * stratum_nf4.h -- C ABI of the MI355X (gfx950) NF4 frozen-weight library.
+ *
+ * One shared library, libstratum_nf4.so, built from the .hip sources in stratum_amd/csrc.
+ * Every entry point:
+ *   - takes plain device pointers, element counts and a HIP stream handle
+ *     (hipStream_t passed as void*, NULL = the null stream);
+ *   - is asynchronous on that stream, allocates nothing and keeps no state
+ *     between calls (the caller keeps buffers alive until the stream is done);
+ *   - never throws; returns STM_OK (0) or a negative STM_ERR_* code, with a
+ *     human-readable reason available from stm_last_error() on the same thread.
+ *
+ * Layout (identical to bitsandbytes' NF4 layout that the reference stores in
+ * NF4Payload, stratum/upload.py:70-95):
+ *   packed : uint8 [(n + 1) / 2]       two 4-bit codes per byte, element 2i in the
+ *                                       high nibble, element 2i+1 in the low nibble
+ *   absmax : float [ceil(n / blocksize)] per-block max|x| (fp32), blocks of
+ *                                       `blocksize` consecutive row-major elements
+ *   code   : the 16 NF4 levels (fixed; the kernels carry them, no code pointer)
+ * A weight W[N, K] is flattened row-major, so with K % blocksize == 0 the
+ * absmax of element (n, k) is absmax[n * (K / blocksize) + k / blocksize].
+ */
+#ifndef STRATUM_NF4_H
+#define STRATUM_NF4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STM_NF4_ABI_VERSION 1
+
+/* return codes */
+#define STM_OK 0
+#define STM_ERR_INVALID (-1)     /* bad argument (null pointer, size, blocksize, dtype, alignment) */
+#define STM_ERR_UNSUPPORTED (-2) /* valid but not handled by this kernel (shape constraint) */
+#define STM_ERR_HIP (-3)         /* a HIP runtime call failed (launch error) */
+
+/* element types */
+#define STM_F16 0
+#define STM_BF16 1
+#define STM_F32 2
+
+/* nearest-level rules of the two bitsandbytes NF4 quantizers */
+#define STM_NF4_ARGMIN 0    /* torch/CPU backend: clamp, first argmin of fp32 |s - code| */
+#define STM_NF4_THRESHOLD 1 /* CUDA kernel: fp32 midpoint comparison tree with strict '>' */
+
+/* Library version (STM_NF4_ABI_VERSION). Host-only, never touches a GPU. */
+int stm_nf4_abi_version(void);
+
+/* Reason for the last non-zero return on the calling thread ("" if none). */
+const char* stm_last_error(void);
+
+/*
+ * Blockwise NF4 quantize + nibble pack.
+ * Replaces bitsandbytes.functional.quantize_4bit(A, blocksize=64,
+ * compress_statistics=False, quant_type="nf4") as called at
+ * stratum/upload.py:367-369 (prepare_nf4) and stratum/upload.py:725-727
+ * (stream_load_and_quantize_module).
+ *   A        : device, n elements of `dtype` (STM_F16 / STM_BF16 / STM_F32), row-major
+ *   blocksize: power of two in [64, 4096]
+ *   rounding : STM_NF4_ARGMIN or STM_NF4_THRESHOLD
+ *   packed   : device, (n + 1) / 2 bytes        absmax: device, ceil(n / blocksize) floats
+ */
+int stm_nf4_quantize(const void* A, int dtype, int64_t n, int blocksize, int rounding, uint8_t* packed,
+                     float* absmax, void* stream);
+
+/*
+ * Blockwise NF4 dequantize: out[i] = dtype(fp32(code[q_i]) * absmax[i / blocksize]),
+ * one fp32 product then one round-to-nearest-even conversion.
+ * Replaces bitsandbytes.functional.dequantize_4bit(q, QuantState(...)) as called at
+ * stratum/upload.py:1038 (ensure_weights), :221 (NF4Prefetch.finalize), :946
+ * (upload_stream) and stratum/nf4_linear.py:46 (NF4Linear.forward).
+ *   out: device, n elements of out_dtype (STM_F16 / STM_BF16 / STM_F32)
+ */
+int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int blocksize, void* out,
+                       int out_dtype, void* stream);
+
+/*
+ * Fused NF4 dequant-GEMM, forward of a frozen Linear:
+ *   Y[M, N] = X[M, K] . W[N, K]^T  (+ bias[N])  (+ T[M, R] . L[N, R]^T)
+ * with W given as NF4 (packed [N*K/2], absmax [N*K/blocksize]) and dequantized
+ * tile by tile in LDS with exactly the dequantize rounding above, fp32
+ * accumulation on bf16/fp16 MFMA.
+ * Replaces F.linear(x, dequantize_4bit(W), bias) at stratum/nf4_linear.py:46-47
+ * (and the F.linear that HF/PEFT modules run on the dequantized param.data,
+ * stratum/stage.py:135). The optional rank-R term is the LoRA update
+ * (T = scale * X . A^T, L = B) that PEFT adds on top of the frozen base.
+ *   dtype        : STM_BF16 or STM_F16, for X, Y, bias, T, L and the dequantized W
+ *   X, Y         : row-major, leading dimensions K and N
+ *   bias         : NULL or [N];  T, L: NULL (lora_rank = 0) or [M, R], [N, R], R % 16 == 0
+ *   constraints  : K % 64 == 0, K % blocksize == 0, all pointers 16-byte aligned
+ */
+int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
+                     const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K, int blocksize,
+                     int dtype, void* stream);
+
+/*
+ * Fused NF4 dequant-GEMM, input gradient of a frozen Linear (no dW: the base
+ * weight has requires_grad=False, stratum/upload.py:328-329):
+ *   dX[M, K] = dY[M, N] . W[N, K]  (+ U[M, R] . At[K, R]^T)
+ * Replaces the autograd backward of F.linear on the dequantized weight, run by
+ * torch.autograd.backward at stratum/runtime.py:340-341. The optional rank-R term
+ * is the LoRA input gradient (U = scale * dY . B, At = A^T).
+ *   constraints  : N % 64 == 0, K % 64 == 0, K % blocksize == 0, 16-byte aligned
+ */
+int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const void* U, const void* At,
+                        int lora_rank, void* dX, int64_t M, int64_t N, int64_t K, int blocksize, int dtype,
+                        void* stream);
+
+/*
+ * Grouped fused NF4 dequant-GEMM over a stacked expert payload, forward:
+ *   for each expert e: Y[off[e]:off[e+1], :] = X[off[e]:off[e+1], :] . W_e^T
+ * where W is one NF4 payload of the stacked tensor [E, N, K] (the layout
+ * prepare_nf4 produces for 3-D MoE weights, stratum/upload.py:365-366) and X/Y
+ * rows are grouped by expert. Replaces the per-expert F.linear loop of
+ * transformers' Qwen3MoeExperts.forward on the dequantized stacked weight.
+ *   offsets: device int32 [E + 1], offsets[0] = 0, non-decreasing, offsets[E] = M_total
+ *   max_rows: an upper bound on offsets[e+1] - offsets[e] (sizes the launch grid)
+ *   constraints: as stm_nf4_gemm_fwd
+ */
+int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const int32_t* offsets,
+                             int num_experts, int64_t max_rows, void* Y, int64_t N, int64_t K, int blocksize,
+                             int dtype, void* stream);
+
+/*
+ * Grouped input gradient: for each expert e: dX[rows of e] = dY[rows of e] . W_e.
+ */
+int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const int32_t* offsets,
+                                int num_experts, int64_t max_rows, void* dX, int64_t N, int64_t K, int blocksize,
+                                int dtype, void* stream);
+
+/*
+ * Host-only introspection used by the CPU test suite (no GPU work):
+ * the 15 fp32 decision boundaries of a rounding rule (code > i iff s >= b[i]),
+ * and the 65-cell table the quantize kernel indexes with
+ * j = (int)(clamp(s, -1, 1) * 32 + 32); code = base[j] + (s >= bound[j]).
+ */
+int stm_nf4_decision_boundaries(int rounding, float* out15);
+int stm_nf4_cell_table(int rounding, float* bound65, uint8_t* base65);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATUM_NF4_H */

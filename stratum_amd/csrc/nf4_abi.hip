@@ -1,0 +1,250 @@
+// extern "C" entry points of libstratum_nf4.so: argument validation, error
+// reporting, the decision-boundary tables, and dispatch to the kernels.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "nf4_common.h"
+#include "nf4_kernels.h"
+
+namespace stm {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(STM_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return STM_OK;
+}
+
+// ---------------------------------------------------------------- boundaries
+// fp32 values ordered as integers (monotone in the float order, -0 == +0 side by side).
+static int64_t fkey(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return (u & 0x80000000u) ? -(int64_t)(u & 0x7FFFFFFFu) : (int64_t)u;
+}
+static float from_key(int64_t k) {
+    uint32_t u = k >= 0 ? (uint32_t)k : (0x80000000u | (uint32_t)(-k));
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+// argmin rule between level i and i+1: level i+1 wins iff its fp32 distance is strictly smaller.
+static bool upper_wins(float s, int i) { return fabsf(s - kLevelsHost[i + 1]) < fabsf(s - kLevelsHost[i]); }
+
+int decision_boundaries(int rounding, float out[15]) {
+    for (int i = 0; i < 15; ++i) {
+        if (rounding == STM_NF4_THRESHOLD) {
+            float t = (float)(((double)kLevelsHost[i] + (double)kLevelsHost[i + 1]) * 0.5);
+            out[i] = nextafterf(t, INFINITY);  // s > t  <=>  s >= next(t)
+        } else if (rounding == STM_NF4_ARGMIN) {
+            int64_t lo = fkey(kLevelsHost[i]), hi = fkey(kLevelsHost[i + 1]);  // P(lo) false, P(hi) true
+            while (hi - lo > 1) {
+                int64_t mid = lo + (hi - lo) / 2;
+                if (upper_wins(from_key(mid), i))
+                    hi = mid;
+                else
+                    lo = mid;
+            }
+            out[i] = from_key(hi);
+        } else {
+            return set_error(STM_ERR_INVALID, "unknown rounding rule %d", rounding);
+        }
+    }
+    return STM_OK;
+}
+
+int build_cell_table(int rounding, CellTable* tab) {
+    float b[15];
+    int rc = decision_boundaries(rounding, b);
+    if (rc) return rc;
+    for (int j = 0; j <= 64; ++j) {
+        // s values that can land in cell j, widened by 1/64 of a cell on both sides
+        double lo = (j - 1.0 / 64) / 32.0 - 1.0, hi = (j + 1.0 + 1.0 / 64) / 32.0 - 1.0;
+        uint32_t base = 0;
+        int inside = 0;
+        float bound = 2.0f;  // never reached: clamped s <= 1
+        for (int i = 0; i < 15; ++i) {
+            if ((double)b[i] <= lo)
+                ++base;
+            else if ((double)b[i] <= hi) {
+                ++inside;
+                bound = b[i];
+            }
+        }
+        if (inside > 1) return set_error(STM_ERR_INVALID, "cell %d holds %d boundaries", j, inside);
+        tab->bound[j] = bound;
+        tab->base[j] = base;
+    }
+    return STM_OK;
+}
+
+static const CellTable* cell_table(int rounding) {
+    static CellTable tabs[2];
+    static int ready[2] = {0, 0};
+    if (rounding < 0 || rounding > 1) return nullptr;
+    if (!ready[rounding]) {  // deterministic; a racing first call just rebuilds the same bytes
+        CellTable t;
+        if (build_cell_table(rounding, &t)) return nullptr;
+        tabs[rounding] = t;
+        ready[rounding] = 1;
+    }
+    return &tabs[rounding];
+}
+
+static bool is_16bit(int dt) { return dt == STM_F16 || dt == STM_BF16; }
+static bool valid_dtype(int dt) { return dt == STM_F16 || dt == STM_BF16 || dt == STM_F32; }
+static bool valid_blocksize(int bs) { return bs >= 64 && bs <= 4096 && is_pow2(bs); }
+
+}  // namespace stm
+
+using namespace stm;
+
+extern "C" {
+
+int stm_nf4_abi_version(void) { return STM_NF4_ABI_VERSION; }
+
+const char* stm_last_error(void) { return g_err; }
+
+int stm_nf4_decision_boundaries(int rounding, float* out15) {
+    if (!out15) return set_error(STM_ERR_INVALID, "out15 is NULL");
+    return decision_boundaries(rounding, out15);
+}
+
+int stm_nf4_cell_table(int rounding, float* bound65, uint8_t* base65) {
+    if (!bound65 || !base65) return set_error(STM_ERR_INVALID, "NULL output");
+    const CellTable* t = cell_table(rounding);
+    if (!t) return set_error(STM_ERR_INVALID, "unknown rounding rule %d", rounding);
+    for (int j = 0; j < 65; ++j) {
+        bound65[j] = t->bound[j];
+        base65[j] = (uint8_t)t->base[j];
+    }
+    return STM_OK;
+}
+
+int stm_nf4_quantize(const void* A, int dtype, int64_t n, int blocksize, int rounding, uint8_t* packed,
+                     float* absmax, void* stream) {
+    g_err[0] = 0;
+    if (n < 0) return set_error(STM_ERR_INVALID, "quantize: n = %lld < 0", (long long)n);
+    if (!valid_dtype(dtype)) return set_error(STM_ERR_INVALID, "quantize: bad dtype %d", dtype);
+    if (!valid_blocksize(blocksize))
+        return set_error(STM_ERR_INVALID, "quantize: blocksize %d not a power of two in [64, 4096]", blocksize);
+    const CellTable* tab = cell_table(rounding);
+    if (!tab) return set_error(STM_ERR_INVALID, "quantize: unknown rounding rule %d", rounding);
+    if (n == 0) return STM_OK;
+    if (!A || !packed || !absmax) return set_error(STM_ERR_INVALID, "quantize: NULL pointer");
+    return launch_quantize(A, dtype, n, blocksize, *tab, packed, absmax, (hipStream_t)stream);
+}
+
+int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int blocksize, void* out,
+                       int out_dtype, void* stream) {
+    g_err[0] = 0;
+    if (n < 0) return set_error(STM_ERR_INVALID, "dequantize: n = %lld < 0", (long long)n);
+    if (!valid_dtype(out_dtype)) return set_error(STM_ERR_INVALID, "dequantize: bad dtype %d", out_dtype);
+    if (!valid_blocksize(blocksize))
+        return set_error(STM_ERR_INVALID, "dequantize: blocksize %d not a power of two in [64, 4096]", blocksize);
+    if (n == 0) return STM_OK;
+    if (!packed || !absmax || !out) return set_error(STM_ERR_INVALID, "dequantize: NULL pointer");
+    return launch_dequantize(packed, absmax, n, blocksize, out, out_dtype, (hipStream_t)stream);
+}
+
+static int check_gemm_common(const char* who, const void* a, const uint8_t* packed, const float* absmax,
+                             const void* out, int64_t M, int64_t N, int64_t K, int blocksize, int dtype) {
+    if (!is_16bit(dtype)) return set_error(STM_ERR_INVALID, "%s: dtype %d is not bf16/fp16", who, dtype);
+    if (M < 0 || N < 0 || K < 0) return set_error(STM_ERR_INVALID, "%s: negative size", who);
+    if (!valid_blocksize(blocksize)) return set_error(STM_ERR_INVALID, "%s: bad blocksize %d", who, blocksize);
+    if (K % 64 != 0 || K % blocksize != 0)
+        return set_error(STM_ERR_UNSUPPORTED, "%s: K = %lld must be a multiple of 64 and of blocksize %d", who,
+                         (long long)K, blocksize);
+    if (M == 0 || N == 0) return STM_OK;
+    if (!a || !packed || !absmax || !out) return set_error(STM_ERR_INVALID, "%s: NULL pointer", who);
+    if (!aligned(a, 16) || !aligned(out, 16) || !aligned(packed, 16) || !aligned(absmax, 4))
+        return set_error(STM_ERR_INVALID, "%s: operands must be 16-byte aligned", who);
+    return 1;  // proceed
+}
+
+int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
+                     const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K, int blocksize,
+                     int dtype, void* stream) {
+    g_err[0] = 0;
+    int rc = check_gemm_common("gemm_fwd", X, packed, absmax, Y, M, N, K, blocksize, dtype);
+    if (rc <= 0) return rc;
+    if (N % 8 != 0) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: N = %lld must be a multiple of 8", (long long)N);
+    if (lora_rank < 0 || lora_rank % 16 != 0 || lora_rank > 256)
+        return set_error(STM_ERR_INVALID, "gemm_fwd: lora_rank %d must be a multiple of 16 in [0, 256]", lora_rank);
+    if (lora_rank > 0 && (!T || !L || !aligned(T, 16) || !aligned(L, 16)))
+        return set_error(STM_ERR_INVALID, "gemm_fwd: lora_rank > 0 needs 16-byte aligned T and L");
+    if (bias && !aligned(bias, 2)) return set_error(STM_ERR_INVALID, "gemm_fwd: misaligned bias");
+    GemmArgs g{};
+    g.a = X; g.packed = packed; g.absmax = absmax; g.bias = bias; g.lora_x = lora_rank ? T : nullptr;
+    g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
+    g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
+    return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
+}
+
+int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const void* U, const void* At,
+                        int lora_rank, void* dX, int64_t M, int64_t N, int64_t K, int blocksize, int dtype,
+                        void* stream) {
+    g_err[0] = 0;
+    int rc = check_gemm_common("gemm_bwd_dx", dY, packed, absmax, dX, M, N, K, blocksize, dtype);
+    if (rc <= 0) return rc;
+    if (N % 64 != 0)
+        return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: N = %lld must be a multiple of 64", (long long)N);
+    if (lora_rank < 0 || lora_rank % 16 != 0 || lora_rank > 256)
+        return set_error(STM_ERR_INVALID, "gemm_bwd_dx: lora_rank %d must be a multiple of 16 in [0, 256]",
+                         lora_rank);
+    if (lora_rank > 0 && (!U || !At || !aligned(U, 16) || !aligned(At, 16)))
+        return set_error(STM_ERR_INVALID, "gemm_bwd_dx: lora_rank > 0 needs 16-byte aligned U and At");
+    GemmArgs g{};
+    g.a = dY; g.packed = packed; g.absmax = absmax; g.bias = nullptr; g.lora_x = lora_rank ? U : nullptr;
+    g.lora_w = lora_rank ? At : nullptr; g.lora_rank = lora_rank; g.out = dX; g.M = M; g.N = N; g.K = K;
+    g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
+    return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
+}
+
+int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const int32_t* offsets,
+                             int num_experts, int64_t max_rows, void* Y, int64_t N, int64_t K, int blocksize,
+                             int dtype, void* stream) {
+    g_err[0] = 0;
+    if (num_experts <= 0 || max_rows < 0)
+        return set_error(STM_ERR_INVALID, "grouped_gemm_fwd: num_experts %d, max_rows %lld", num_experts,
+                         (long long)max_rows);
+    int rc = check_gemm_common("grouped_gemm_fwd", X, packed, absmax, Y, max_rows, N, K, blocksize, dtype);
+    if (rc <= 0) return rc;
+    if (!offsets) return set_error(STM_ERR_INVALID, "grouped_gemm_fwd: NULL offsets");
+    if (N % 8 != 0) return set_error(STM_ERR_UNSUPPORTED, "grouped_gemm_fwd: N must be a multiple of 8");
+    GemmArgs g{};
+    g.a = X; g.packed = packed; g.absmax = absmax; g.out = Y; g.M = max_rows; g.N = N; g.K = K;
+    g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
+    return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
+}
+
+int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const int32_t* offsets,
+                                int num_experts, int64_t max_rows, void* dX, int64_t N, int64_t K, int blocksize,
+                                int dtype, void* stream) {
+    g_err[0] = 0;
+    if (num_experts <= 0 || max_rows < 0)
+        return set_error(STM_ERR_INVALID, "grouped_gemm_bwd_dx: num_experts %d, max_rows %lld", num_experts,
+                         (long long)max_rows);
+    int rc = check_gemm_common("grouped_gemm_bwd_dx", dY, packed, absmax, dX, max_rows, N, K, blocksize, dtype);
+    if (rc <= 0) return rc;
+    if (!offsets) return set_error(STM_ERR_INVALID, "grouped_gemm_bwd_dx: NULL offsets");
+    if (N % 64 != 0) return set_error(STM_ERR_UNSUPPORTED, "grouped_gemm_bwd_dx: N must be a multiple of 64");
+    GemmArgs g{};
+    g.a = dY; g.packed = packed; g.absmax = absmax; g.out = dX; g.M = max_rows; g.N = N; g.K = K;
+    g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
+    return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
+}
+
+}  // extern "C"

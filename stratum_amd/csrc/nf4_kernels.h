@@ -1,0 +1,36 @@
+// Launchers implemented by the kernel translation units.
+#pragma once
+
+#include "nf4_common.h"
+
+namespace stm {
+
+// One description for the dense and the grouped (per-expert) GEMMs.
+//   forward : out[M, N] = a[M, K] . W[N, K]^T (+ bias) (+ lora_x[M, R] . lora_w[N, R]^T)
+//   backward: out[M, K] = a[M, N] . W[N, K]        (+ lora_x[M, R] . lora_w[K, R]^T)
+// Grouped: `offsets` (device int32 [num_groups + 1]) splits the rows of a/out by
+// expert; expert e uses the e-th [N, K] slice of the stacked NF4 payload and M
+// is the largest row count of any expert.
+struct GemmArgs {
+    const void* a;
+    const uint8_t* packed;
+    const float* absmax;
+    const void* bias;
+    const void* lora_x;
+    const void* lora_w;
+    int lora_rank;
+    void* out;
+    int64_t M, N, K;
+    int blocksize;
+    const int32_t* offsets;
+    int num_groups;
+};
+
+int launch_quantize(const void* A, int dtype, int64_t n, int blocksize, const CellTable& tab, uint8_t* packed,
+                    float* absmax, hipStream_t stream);
+int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int blocksize, void* out, int out_dtype,
+                      hipStream_t stream);
+int launch_gemm_fwd(const GemmArgs& g, int dtype, hipStream_t stream);
+int launch_gemm_bwd(const GemmArgs& g, int dtype, hipStream_t stream);
+
+}  // namespace stm

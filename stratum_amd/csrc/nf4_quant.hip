@@ -1,0 +1,288 @@
+// NF4 blockwise quantize + nibble pack, and dequantize, for gfx950.
+//
+// quantize: one lane owns 8 consecutive elements (one 16-byte load of fp16/bf16),
+//   the L = blocksize/8 lanes of a block reduce max|x| with cross-lane shuffles,
+//   every element picks its level from a 65-cell table held in LDS, and each
+//   lane stores its 8 codes as one 32-bit word, so a wave writes 256 contiguous
+//   bytes of packed codes per iteration.
+// dequantize: one lane owns one 32-bit word of packed codes (8 elements), looks
+//   each byte up in a 256-entry (level_hi, level_lo) table in LDS, multiplies by
+//   the block's absmax in fp32 and stores 16 bytes of fp16/bf16 (32 of fp32).
+#include <type_traits>
+
+#include "nf4_kernels.h"
+
+namespace stm {
+
+#pragma clang fp contract(off)
+
+template <int DT>
+using Tr16 = std::conditional_t<DT == STM_BF16, BF16, F16>;
+
+__device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
+
+// clamp to [-1, 1] (NaN -> -1, which the table maps to code 0 like both rules do)
+__device__ __forceinline__ uint32_t level_of(float s, const float* __restrict__ bound,
+                                             const uint32_t* __restrict__ base) {
+    float c = (s >= -1.0f) ? ((s <= 1.0f) ? s : 1.0f) : -1.0f;
+    int j = (int)(c * 32.0f + 32.0f);
+    return base[j] + (c >= bound[j] ? 1u : 0u);
+}
+
+template <int DT>
+__device__ __forceinline__ float load1(const void* x, int64_t i) {
+    if constexpr (DT == STM_F32)
+        return reinterpret_cast<const float*>(x)[i];
+    else
+        return Tr16<DT>::to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
+}
+
+// elements 8g .. 8g+7
+template <int DT>
+__device__ __forceinline__ void load8(const void* __restrict__ x, int64_t g, float* v) {
+    if constexpr (DT == STM_F32) {
+        const float4* p = reinterpret_cast<const float4*>(x) + 2 * g;
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        uint4 w = reinterpret_cast<const uint4*>(x)[g];
+        uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = Tr16<DT>::to_f32((uint16_t)(u[k] & 0xFFFFu));
+            v[2 * k + 1] = Tr16<DT>::to_f32((uint16_t)(u[k] >> 16));
+        }
+    }
+}
+
+// L lanes per quantization block, C 8-element chunks per lane: blocksize = 8 * L * C.
+template <int DT, int L, int C>
+__global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
+                                                  float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
+    __shared__ float s_bound[65];
+    __shared__ uint32_t s_base[65];
+    if (threadIdx.x < 65) {
+        s_bound[threadIdx.x] = tab.bound[threadIdx.x];
+        s_base[threadIdx.x] = tab.base[threadIdx.x];
+    }
+    __syncthreads();
+
+    constexpr int BPW = 64 / L;       // blocks per wave iteration
+    constexpr int GPB = L * C;        // 8-element groups per block
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+    const int64_t nwaves = (int64_t)gridDim.x * 4;
+
+    for (int64_t b0 = wave * BPW; b0 < nblocks; b0 += nwaves * BPW) {
+        const int64_t blk = b0 + lane / L;
+        const bool active = blk < nblocks;
+        float v[C][8];
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int64_t g = blk * GPB + c * L + (lane % L);
+            if (active) {
+                load8<DT>(x, g, v[c]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[c][e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = nanmax(a, fabsf(v[c][e]));
+        }
+#pragma unroll
+        for (int off = 1; off < L; off <<= 1) a = nanmax(a, __shfl_xor(a, off));
+        const float r = 1.0f / a;  // IEEE division (correctly rounded)
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t q0 = level_of(v[c][2 * p] * r, s_bound, s_base);
+                uint32_t q1 = level_of(v[c][2 * p + 1] * r, s_bound, s_base);
+                word |= ((q0 << 4) | q1) << (8 * p);
+            }
+            if (active) packed[blk * GPB + c * L + (lane % L)] = word;
+        }
+        if (active && (lane % L) == 0) absmax[blk] = a;
+    }
+}
+
+// One thread per block; used for a partial last block and for unaligned inputs.
+template <int DT>
+__global__ __launch_bounds__(64) void k_quantize_generic(const void* __restrict__ x, int64_t n, int bs,
+                                                         int64_t b_begin, int64_t b_end, uint8_t* __restrict__ packed,
+                                                         float* __restrict__ absmax, CellTable tab) {
+    __shared__ float s_bound[65];
+    __shared__ uint32_t s_base[65];
+    for (int t = threadIdx.x; t < 65; t += 64) {
+        s_bound[t] = tab.bound[t];
+        s_base[t] = tab.base[t];
+    }
+    __syncthreads();
+    const int64_t blk = b_begin + (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (blk >= b_end) return;
+    const int64_t lo = blk * bs, hi = (lo + bs < n) ? lo + bs : n;
+    float a = 0.0f;
+    for (int64_t i = lo; i < hi; ++i) a = nanmax(a, fabsf(load1<DT>(x, i)));
+    absmax[blk] = a;
+    const float r = 1.0f / a;
+    for (int64_t i = lo; i < hi; i += 2) {
+        uint32_t q0 = level_of(load1<DT>(x, i) * r, s_bound, s_base);
+        uint32_t q1 = (i + 1 < hi) ? level_of(load1<DT>(x, i + 1) * r, s_bound, s_base) : 0u;
+        packed[i >> 1] = (uint8_t)((q0 << 4) | q1);
+    }
+}
+
+template <int DT>
+static void quantize_vec_dispatch(const void* A, int64_t nfull, int bs, const CellTable& tab, uint8_t* packed,
+                                  float* absmax, hipStream_t stream) {
+    // one wave handles 64/L blocks per iteration; size the grid to ~8 iterations per wave
+    const int L = bs >= 512 ? 64 : bs / 8;
+    const int64_t per_wave = 64 / L;
+    int64_t waves = (nfull + per_wave - 1) / per_wave;
+    int64_t grid = (waves + 4 * 8 - 1) / (4 * 8);
+    if (grid < 1) grid = 1;
+    if (grid > 65535) grid = 65535;
+    uint32_t* p4 = reinterpret_cast<uint32_t*>(packed);
+    dim3 g((unsigned)grid), b(256);
+    switch (bs) {
+        case 64: hipLaunchKernelGGL((k_quantize<DT, 8, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 128: hipLaunchKernelGGL((k_quantize<DT, 16, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 256: hipLaunchKernelGGL((k_quantize<DT, 32, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 512: hipLaunchKernelGGL((k_quantize<DT, 64, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 1024: hipLaunchKernelGGL((k_quantize<DT, 64, 2>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 2048: hipLaunchKernelGGL((k_quantize<DT, 64, 4>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        default: hipLaunchKernelGGL((k_quantize<DT, 64, 8>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+    }
+}
+
+int launch_quantize(const void* A, int dtype, int64_t n, int bs, const CellTable& tab, uint8_t* packed,
+                    float* absmax, hipStream_t stream) {
+    const int64_t nblocks = (n + bs - 1) / bs;
+    const bool vec_ok = aligned(A, 16) && aligned(packed, 4);
+    const int64_t nfull = vec_ok ? n / bs : 0;
+    if (nfull > 0) {
+        if (dtype == STM_F16)
+            quantize_vec_dispatch<STM_F16>(A, nfull, bs, tab, packed, absmax, stream);
+        else if (dtype == STM_BF16)
+            quantize_vec_dispatch<STM_BF16>(A, nfull, bs, tab, packed, absmax, stream);
+        else
+            quantize_vec_dispatch<STM_F32>(A, nfull, bs, tab, packed, absmax, stream);
+        int rc = check_launch("quantize");
+        if (rc) return rc;
+    }
+    if (nfull < nblocks) {
+        dim3 g((unsigned)((nblocks - nfull + 63) / 64)), b(64);
+        if (dtype == STM_F16)
+            hipLaunchKernelGGL(k_quantize_generic<STM_F16>, g, b, 0, stream, A, n, bs, nfull, nblocks, packed, absmax, tab);
+        else if (dtype == STM_BF16)
+            hipLaunchKernelGGL(k_quantize_generic<STM_BF16>, g, b, 0, stream, A, n, bs, nfull, nblocks, packed, absmax, tab);
+        else
+            hipLaunchKernelGGL(k_quantize_generic<STM_F32>, g, b, 0, stream, A, n, bs, nfull, nblocks, packed, absmax, tab);
+        return check_launch("quantize(tail)");
+    }
+    return STM_OK;
+}
+
+// ------------------------------------------------------------------ dequant
+template <int DT>
+__device__ __forceinline__ void store8(void* __restrict__ out, int64_t g, const float* v) {
+    if constexpr (DT == STM_F32) {
+        float4* o = reinterpret_cast<float4*>(out) + 2 * g;
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        uint4 r;
+        r.x = Tr16<DT>::pack2(v[0], v[1]);
+        r.y = Tr16<DT>::pack2(v[2], v[3]);
+        r.z = Tr16<DT>::pack2(v[4], v[5]);
+        r.w = Tr16<DT>::pack2(v[6], v[7]);
+        reinterpret_cast<uint4*>(out)[g] = r;
+    }
+}
+
+// U words of packed codes per lane, wave-contiguous: word g = (block*U + j)*256 + tid.
+template <int DT, int U>
+__global__ __launch_bounds__(256) void k_dequantize(const uint32_t* __restrict__ q, const float* __restrict__ absmax,
+                                                    void* __restrict__ out, int64_t ngroups, int gshift) {
+    __shared__ float2 lut[256];
+    lut[threadIdx.x] = make_float2(kLevelsDev[threadIdx.x >> 4], kLevelsDev[threadIdx.x & 15]);
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * (U * 256) + threadIdx.x;
+    uint32_t w[U];
+    float a[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t g = base + j * 256;
+        w[j] = 0u;
+        a[j] = 0.0f;
+        if (g < ngroups) {
+            w[j] = q[g];
+            a[j] = absmax[g >> gshift];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t g = base + j * 256;
+        if (g < ngroups) {
+            float v[8];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float2 c = lut[(w[j] >> (8 * b)) & 0xFFu];
+                v[2 * b] = opaque(c.x * a[j]);
+                v[2 * b + 1] = opaque(c.y * a[j]);
+            }
+            store8<DT>(out, g, v);
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_dequantize_generic(const uint8_t* __restrict__ q,
+                                                            const float* __restrict__ absmax, void* __restrict__ out,
+                                                            int64_t start, int64_t n, int bshift) {
+    const int64_t i = start + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t byte = q[i >> 1];
+    const uint32_t code = (i & 1) ? (byte & 15u) : (byte >> 4);
+    const float v = opaque(kLevelsDev[code] * absmax[i >> bshift]);
+    if constexpr (DT == STM_F32)
+        reinterpret_cast<float*>(out)[i] = v;
+    else
+        reinterpret_cast<uint16_t*>(out)[i] = Tr16<DT>::from_f32(v);
+}
+
+template <int DT>
+static void dequant_dispatch(const uint8_t* packed, const float* absmax, int64_t n, int bshift, void* out,
+                             bool vec_ok, hipStream_t stream) {
+    constexpr int U = 4;
+    const int64_t ngroups = vec_ok ? n / 8 : 0;
+    if (ngroups > 0) {
+        dim3 g((unsigned)((ngroups + U * 256 - 1) / (U * 256))), b(256);
+        hipLaunchKernelGGL((k_dequantize<DT, U>), g, b, 0, stream, reinterpret_cast<const uint32_t*>(packed), absmax,
+                           out, ngroups, bshift - 3);
+    }
+    const int64_t start = ngroups * 8;
+    if (start < n) {
+        dim3 g((unsigned)((n - start + 255) / 256)), b(256);
+        hipLaunchKernelGGL(k_dequantize_generic<DT>, g, b, 0, stream, packed, absmax, out, start, n, bshift);
+    }
+}
+
+int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int bs, void* out, int out_dtype,
+                      hipStream_t stream) {
+    const int bshift = ilog2(bs);
+    const bool vec_ok = aligned(packed, 4) && aligned(out, 16);
+    if ((n + 255) / 256 > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "dequantize: n too large");
+    if (out_dtype == STM_F16)
+        dequant_dispatch<STM_F16>(packed, absmax, n, bshift, out, vec_ok, stream);
+    else if (out_dtype == STM_BF16)
+        dequant_dispatch<STM_BF16>(packed, absmax, n, bshift, out, vec_ok, stream);
+    else
+        dequant_dispatch<STM_F32>(packed, absmax, n, bshift, out, vec_ok, stream);
+    return check_launch("dequantize");
+}
+
+}  // namespace stm

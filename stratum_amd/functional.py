@@ -1,0 +1,291 @@
+"""NF4 operators on the gfx950 kernels, shaped like the ``bitsandbytes.functional``
+API that the reference calls (``quantize_4bit``, ``dequantize_4bit``,
+``QuantState``, ``get_4bit_type``), plus the fused frozen-base GEMMs.
+
+Reference call sites this module replaces:
+  quantize_4bit   stratum/upload.py:367-369, :725-727; scripts/doctor.py:80-85
+  dequantize_4bit stratum/upload.py:221, :946, :1038; stratum/nf4_linear.py:46
+  F.linear on the dequantized frozen weight, forward and input gradient:
+                  stratum/nf4_linear.py:47, stratum/stage.py:135,
+                  stratum/runtime.py:340-341, stratum/model/mlp_opt.py:181-183,206-212
+
+Every operator runs the HIP library; there is no CPU implementation. A CPU
+input to ``quantize_4bit`` is copied to the current GPU, quantized there and
+copied back, so the result lands where bitsandbytes' would (on the input's
+device).
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+# NF4 levels (QLoRA, arXiv 2305.14314 App. E); the fp32 table bitsandbytes
+# returns from get_4bit_type("nf4") and the reference stores in NF4Payload.code.
+NF4_LEVELS = (
+    -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+    -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+    0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+    0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0,
+)
+
+ROUNDING_RULES = {"argmin": _lib.STM_NF4_ARGMIN, "threshold": _lib.STM_NF4_THRESHOLD}
+# The reference quantizes CPU tensors (stratum/upload.py:360), i.e. with the
+# torch/CPU backend of bitsandbytes, whose nearest-level rule is an fp32 argmin.
+DEFAULT_ROUNDING = "argmin"
+
+
+def get_4bit_type(typename: str = "nf4", device=None) -> torch.Tensor:
+    if typename != "nf4":
+        raise NotImplementedError(f"4-bit type {typename!r} is not supported (only 'nf4')")
+    return torch.tensor(NF4_LEVELS, dtype=torch.float32, device=device)
+
+
+class QuantState:
+    """Quantization metadata of one NF4 tensor (the fields bitsandbytes'
+    QuantState carries on this path; ``stratum/upload.py:211-218,1031-1034``)."""
+
+    def __init__(self, absmax: torch.Tensor, shape=None, code: Optional[torch.Tensor] = None,
+                 blocksize: Optional[int] = None, quant_type: Optional[str] = None,
+                 dtype: Optional[torch.dtype] = None, offset=None, state2=None):
+        if offset is not None or state2 is not None:
+            raise NotImplementedError("nested (compress_statistics=True) absmax is not supported")
+        self.absmax = absmax
+        self.shape = torch.Size(shape) if shape is not None else None
+        self.code = code if code is not None else get_4bit_type("nf4", device=absmax.device)
+        self.blocksize = int(blocksize) if blocksize is not None else 64
+        self.quant_type = quant_type if quant_type is not None else "nf4"
+        self.dtype = dtype
+        self.offset = None
+        self.state2 = None
+        self.nested = False
+
+    def to(self, device) -> "QuantState":
+        self.absmax = self.absmax.to(device)
+        self.code = self.code.to(device)
+        return self
+
+    def __repr__(self) -> str:
+        return (f"QuantState(shape={tuple(self.shape) if self.shape is not None else None}, "
+                f"dtype={self.dtype}, blocksize={self.blocksize}, quant_type={self.quant_type!r})")
+
+
+def _check_nf4(quant_type: str, blocksize: int) -> None:
+    if quant_type != "nf4":
+        raise NotImplementedError(f"quant_type {quant_type!r} is not supported (only 'nf4')")
+    if blocksize < 64 or blocksize > 4096 or blocksize & (blocksize - 1):
+        raise ValueError(f"blocksize {blocksize} must be a power of two in [64, 4096]")
+
+
+def _gpu_device(t: torch.Tensor) -> torch.device:
+    if t.is_cuda:
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("stratum_amd NF4 kernels need a GPU (HIP); none is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _aligned(t: torch.Tensor, a: int = 16) -> torch.Tensor:
+    t = t.contiguous()
+    if t.numel() and t.data_ptr() % a:
+        t = t.clone()
+    return t
+
+
+@torch.no_grad()
+def quantize_4bit(A: torch.Tensor, absmax: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                  blocksize: int = 64, compress_statistics: bool = False, quant_type: str = "nf4",
+                  quant_storage: torch.dtype = torch.uint8, *, rounding: str = DEFAULT_ROUNDING):
+    """Blockwise NF4 quantize + pack. Returns ``(packed uint8 [(n+1)//2, 1], QuantState)``.
+
+    ``rounding`` picks the nearest-level rule: "argmin" (bitsandbytes' torch/CPU
+    backend, the path the reference runs) or "threshold" (its CUDA kernel);
+    the two differ only for values that sit exactly on an fp32 midpoint.
+    """
+    _check_nf4(quant_type, blocksize)
+    if compress_statistics:
+        raise NotImplementedError("compress_statistics=True is not supported (the reference passes False)")
+    if quant_storage != torch.uint8:
+        raise NotImplementedError("only uint8 quant_storage is supported")
+    if rounding not in ROUNDING_RULES:
+        raise ValueError(f"rounding must be one of {sorted(ROUNDING_RULES)}, got {rounding!r}")
+    tag = _lib.dtype_tag(A.dtype)
+    dev = _gpu_device(A)
+    src = _aligned(A.detach().to(dev))
+    n = src.numel()
+    nblocks = -(-n // blocksize)
+    packed = torch.empty(((n + 1) // 2, 1), dtype=torch.uint8, device=dev)
+    am = torch.empty(nblocks, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        rc = L.stm_nf4_quantize(src.data_ptr(), tag, n, blocksize, ROUNDING_RULES[rounding], packed.data_ptr(),
+                                am.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_quantize")
+    if not A.is_cuda:
+        packed = packed.to(A.device)
+        am = am.to(A.device)
+    if out is not None:
+        out.copy_(packed.view_as(out))
+        packed = out
+    if absmax is not None:
+        absmax.copy_(am)
+        am = absmax
+    state = QuantState(absmax=am, shape=A.shape, code=get_4bit_type("nf4", device=am.device), blocksize=blocksize,
+                       quant_type=quant_type, dtype=A.dtype)
+    return packed, state
+
+
+@torch.no_grad()
+def dequantize_4bit(A: torch.Tensor, quant_state: Optional[QuantState] = None, absmax: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None, blocksize: int = 64, quant_type: str = "nf4",
+                    *, dtype: Optional[torch.dtype] = None, shape: Optional[Sequence[int]] = None) -> torch.Tensor:
+    """``out = dtype(code[q] * absmax)`` for every element, on A's device and the current stream.
+
+    ``dtype`` overrides ``quant_state.dtype`` (e.g. an fp16-sourced payload
+    dequantized to bf16 for bf16 compute).
+    """
+    if quant_state is not None:
+        absmax = quant_state.absmax if absmax is None else absmax
+        blocksize = quant_state.blocksize
+        quant_type = quant_state.quant_type
+        shape = quant_state.shape if shape is None else shape
+        dtype = quant_state.dtype if dtype is None else dtype
+    if absmax is None or shape is None:
+        raise ValueError("dequantize_4bit needs a quant_state or absmax + shape")
+    dtype = dtype or torch.float16
+    _check_nf4(quant_type, blocksize)
+    if not A.is_cuda:
+        raise RuntimeError("dequantize_4bit runs on the GPU kernel; the packed tensor is on the CPU")
+    dev = A.device
+    n = 1
+    for s in shape:
+        n *= int(s)
+    if A.numel() * 2 < n:
+        raise ValueError(f"packed tensor holds {A.numel() * 2} codes, shape {tuple(shape)} needs {n}")
+    if absmax.numel() < -(-n // blocksize):
+        raise ValueError(f"absmax holds {absmax.numel()} blocks, need {-(-n // blocksize)}")
+    q = _aligned(A, 4)
+    am = _aligned(absmax.to(dev, torch.float32), 4)
+    if out is None:
+        out = torch.empty(tuple(shape), dtype=dtype, device=dev)
+    elif not out.is_contiguous() or out.numel() != n or out.dtype != dtype:
+        raise ValueError("out must be a contiguous tensor of the quant_state shape and dtype")
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_nf4_dequantize(q.data_ptr(), am.data_ptr(), n, blocksize, out.data_ptr(),
+                                           _lib.dtype_tag(dtype), _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_dequantize")
+    return out
+
+
+# ------------------------------------------------------------ fused GEMMs
+def _gemm_dtype(t: torch.Tensor) -> int:
+    if t.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"fused NF4 GEMM computes in bf16 or fp16, got {t.dtype}")
+    return _lib.dtype_tag(t.dtype)
+
+
+def fused_supported(N: int, K: int, blocksize: int, backward: bool = False) -> bool:
+    """Shapes the fused kernels take; other shapes go through dequantize + matmul."""
+    if K % 64 or K % blocksize or N % 8:
+        return False
+    return not backward or N % 64 == 0
+
+
+@torch.no_grad()
+def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, weight_shape: Sequence[int],
+                 blocksize: int = 64, bias: Optional[torch.Tensor] = None, lora_t: Optional[torch.Tensor] = None,
+                 lora_b: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x @ W.T (+ bias) (+ lora_t @ lora_b.T)`` with W [N, K] in NF4; output dtype = x.dtype.
+
+    ``W`` is dequantized inside the kernel with the same rounding as
+    ``dequantize_4bit(..., dtype=x.dtype)``. ``lora_t`` [M, R] and ``lora_b`` [N, R]
+    (R a multiple of 16) add a rank-R term before the single output rounding.
+    """
+    N, K = int(weight_shape[0]), int(weight_shape[1])
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects {K}")
+    tag = _gemm_dtype(x)
+    lead = x.shape[:-1]
+    x2 = _aligned(x.reshape(-1, K))
+    M = x2.shape[0]
+    dev = x2.device
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    b = _aligned(bias.to(x.dtype), 2) if bias is not None else None
+    R = 0
+    t = lb = None
+    if lora_t is not None:
+        t = _aligned(lora_t.reshape(M, -1).to(x.dtype))
+        lb = _aligned(lora_b.to(x.dtype))
+        R = t.shape[1]
+        if lb.shape != (N, R):
+            raise ValueError(f"lora_b shape {tuple(lb.shape)} != ({N}, {R})")
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_nf4_gemm_fwd(
+            x2.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(),
+            b.data_ptr() if b is not None else None,
+            t.data_ptr() if t is not None else None, lb.data_ptr() if lb is not None else None, R,
+            y.data_ptr(), M, N, K, blocksize, tag, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_gemm_fwd")
+    return y.reshape(*lead, N)
+
+
+@torch.no_grad()
+def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, weight_shape: Sequence[int],
+                    blocksize: int = 64, lora_u: Optional[torch.Tensor] = None,
+                    lora_at: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``dy @ W (+ lora_u @ lora_at.T)`` with W [N, K] in NF4; output dtype = dy.dtype."""
+    N, K = int(weight_shape[0]), int(weight_shape[1])
+    if dy.shape[-1] != N:
+        raise ValueError(f"dy has {dy.shape[-1]} features, weight has {N} rows")
+    tag = _gemm_dtype(dy)
+    lead = dy.shape[:-1]
+    d2 = _aligned(dy.reshape(-1, N))
+    M = d2.shape[0]
+    dev = d2.device
+    dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
+    R = 0
+    u = at = None
+    if lora_u is not None:
+        u = _aligned(lora_u.reshape(M, -1).to(dy.dtype))
+        at = _aligned(lora_at.to(dy.dtype))
+        R = u.shape[1]
+        if at.shape != (K, R):
+            raise ValueError(f"lora_at shape {tuple(at.shape)} != ({K}, {R})")
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_nf4_gemm_bwd_dx(
+            d2.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(),
+            u.data_ptr() if u is not None else None, at.data_ptr() if at is not None else None, R,
+            dx.data_ptr(), M, N, K, blocksize, tag, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_gemm_bwd_dx")
+    return dx.reshape(*lead, K)
+
+
+@torch.no_grad()
+def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, offsets: torch.Tensor,
+                     expert_shape: Sequence[int], blocksize: int = 64, max_rows: Optional[int] = None,
+                     backward: bool = False) -> torch.Tensor:
+    """Per-expert ``x[rows_e] @ W_e.T`` (or ``@ W_e`` when ``backward``) over a stacked
+    NF4 payload of shape [E, N, K]; ``offsets`` int32 [E + 1] delimits each expert's rows."""
+    E = offsets.numel() - 1
+    N, K = int(expert_shape[0]), int(expert_shape[1])
+    tag = _gemm_dtype(x)
+    xin = _aligned(x)
+    M_total = xin.shape[0]
+    dev = xin.device
+    off = offsets.to(device=dev, dtype=torch.int32).contiguous()
+    if max_rows is None:
+        max_rows = int((off[1:] - off[:-1]).max().item()) if E > 0 else 0
+    out_cols = K if backward else N
+    in_cols = N if backward else K
+    if xin.shape[1] != in_cols:
+        raise ValueError(f"x has {xin.shape[1]} columns, expected {in_cols}")
+    y = torch.empty((M_total, out_cols), dtype=x.dtype, device=dev)
+    fn = _lib.lib().stm_nf4_grouped_gemm_bwd_dx if backward else _lib.lib().stm_nf4_grouped_gemm_fwd
+    with torch.cuda.device(dev):
+        rc = fn(xin.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(), off.data_ptr(), E,
+                int(max_rows), y.data_ptr(), N, K, blocksize, tag, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_grouped_gemm_" + ("bwd_dx" if backward else "fwd"))
+    return y

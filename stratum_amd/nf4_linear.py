@@ -1,0 +1,125 @@
+"""NF4Linear: frozen Linear whose weight stays NF4-packed on the GPU.
+
+Mirrors ``stratum/nf4_linear.py:17-47`` (same constructor, ``in_features`` /
+``out_features`` from ``quant_state.shape``). Where the reference dequantizes the
+whole weight to a temporary fp16 tensor and calls ``F.linear``
+(``stratum/nf4_linear.py:46-47``), forward here is one fused dequant-GEMM and
+backward is one fused dequant-GEMM for ``dX = dY . W`` -- the dequantized weight
+never exists in HBM. ``NF4LoRALinear`` adds the PEFT-style LoRA update
+(``scripts/train.py:568-573``: r=16, alpha=16) with its rank-16 term folded into
+the same two kernels.
+
+Shapes the fused kernels do not take (K not a multiple of 64, ...) and dtypes
+other than bf16/fp16 run ``dequantize_4bit`` + ``F.linear`` on the GPU instead.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .functional import (QuantState, dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd)
+
+
+class _NF4LinearFn(torch.autograd.Function):
+    """y = x . W^T (+ bias) (+ scaling * (x . A^T) . B^T) with W frozen in NF4."""
+
+    @staticmethod
+    def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling):
+        t = None
+        if lora_a is not None:
+            t = (x.reshape(-1, x.shape[-1]) @ lora_a.t().to(x.dtype)) * scaling
+        y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
+                         lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
+        ctx.shape, ctx.blocksize, ctx.scaling = shape, blocksize, scaling
+        ctx.has_bias_grad = bias is not None and bias.requires_grad
+        ctx.save_for_backward(x if lora_a is not None else None, packed, absmax, lora_a, lora_b, t)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, packed, absmax, lora_a, lora_b, t = ctx.saved_tensors
+        N, K = ctx.shape
+        dy2 = dy.reshape(-1, N).contiguous()
+        u = None
+        if lora_a is not None:
+            u = (dy2 @ lora_b.to(dy2.dtype)) * ctx.scaling                  # [M, R]
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = nf4_gemm_bwd_dx(dy2, packed, absmax, ctx.shape, ctx.blocksize, lora_u=u,
+                                 lora_at=lora_a.t().contiguous().to(dy2.dtype) if lora_a is not None else None)
+            dx = dx.reshape(*dy.shape[:-1], K)
+        d_bias = dy2.sum(0).to(dy.dtype) if ctx.has_bias_grad else None
+        d_a = d_b = None
+        if lora_a is not None:
+            x2 = x.reshape(-1, K)
+            if ctx.needs_input_grad[6]:
+                d_a = (u.t() @ x2).to(lora_a.dtype)                         # [R, K]
+            if ctx.needs_input_grad[7]:
+                d_b = (dy2.t() @ t).to(lora_b.dtype)                        # [N, R]
+        return dx, None, None, None, None, d_bias, d_a, d_b, None
+
+
+def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None,
+               lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+               scaling: float = 1.0) -> torch.Tensor:
+    shape = tuple(int(s) for s in quant_state.shape)
+    N, K = shape
+    bs = quant_state.blocksize
+    rank = lora_a.shape[0] if lora_a is not None else 0
+    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and fused_supported(N, K, bs, backward=True)
+            and rank % 16 == 0):
+        return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling)
+    # unfused GPU path: dequantize into a temporary, then the library GEMM
+    w = dequantize_4bit(quantized, quant_state, dtype=x.dtype)
+    y = F.linear(x, w, bias.to(x.dtype) if bias is not None else None)
+    if lora_a is not None:
+        y = y + F.linear(F.linear(x, lora_a.to(x.dtype)), lora_b.to(x.dtype)) * scaling
+    return y
+
+
+class NF4Linear(nn.Module):
+    """Frozen Linear layer with an NF4-compressed weight kept on the GPU.
+
+    Same constructor as the reference (``stratum/nf4_linear.py:27-41``): the
+    packed codes, their ``QuantState`` and an optional bias (stored frozen).
+    """
+
+    def __init__(self, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None):
+        super().__init__()
+        self.quantized = quantized
+        self.quant_state = quant_state
+        if bias is not None:
+            self.bias = nn.Parameter(bias.contiguous(), requires_grad=False)
+        else:
+            self.bias = None
+        self.in_features = quant_state.shape[1]
+        self.out_features = quant_state.shape[0]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return nf4_linear(x, self.quantized, self.quant_state, self.bias)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, nf4 blocksize={self.quant_state.blocksize}"
+
+
+class NF4LoRALinear(NF4Linear):
+    """NF4Linear plus a trainable LoRA update ``scaling * B(A(x))`` (PEFT's
+    ``lora.Linear`` with r, alpha; A ~ kaiming-uniform, B = 0 at init)."""
+
+    def __init__(self, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None, *,
+                 r: int = 16, lora_alpha: float = 16.0, dtype: torch.dtype = torch.bfloat16):
+        super().__init__(quantized, quant_state, bias)
+        dev = quantized.device
+        self.r = r
+        self.scaling = lora_alpha / r
+        self.lora_A = nn.Parameter(torch.empty(r, self.in_features, dtype=dtype, device=dev))
+        self.lora_B = nn.Parameter(torch.zeros(self.out_features, r, dtype=dtype, device=dev))
+        nn.init.kaiming_uniform_(self.lora_A, a=math.sqrt(5))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return nf4_linear(x, self.quantized, self.quant_state, self.bias, self.lora_A, self.lora_B, self.scaling)

@@ -1,0 +1,109 @@
+"""The C ABI library on the CPU: it loads, exports every symbol the header
+declares, rejects bad arguments before touching a GPU, and its host-side
+decision tables agree with the oracle (exhaustively over fp32)."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle as C
+from oracle import nf4_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "stratum_nf4.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from stratum_amd import _lib
+    return _lib.lib()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(stm_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = header_functions()
+    for n in ("stm_nf4_quantize", "stm_nf4_dequantize", "stm_nf4_gemm_fwd", "stm_nf4_gemm_bwd_dx",
+              "stm_nf4_grouped_gemm_fwd", "stm_nf4_grouped_gemm_bwd_dx", "stm_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    from stratum_amd import _lib
+    missing = [n for n in header_functions() if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(header_functions()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version(L):
+    assert L.stm_nf4_abi_version() == 1
+
+
+@pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
+def test_boundaries_match_oracle(L, rule, code):
+    out = np.zeros(15, np.float32)
+    assert L.stm_nf4_decision_boundaries(code, out.ctypes.data) == 0
+    np.testing.assert_array_equal(out.view(np.uint32), O.decision_boundaries(rule).view(np.uint32))
+
+
+@pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
+def test_cell_table_is_exact_over_all_fp32(L, rule, code):
+    """Every fp32 s in [-1, 1] (plus NaN, +-inf, values just outside) gets the
+    same level from the kernel's 65-cell table as from the C restatement."""
+    bound = np.zeros(65, np.float32)
+    base = np.zeros(65, np.uint8)
+    assert L.stm_nf4_cell_table(code, bound.ctypes.data, base.ctypes.data) == 0
+    bad, first = C.check_cells(bound, base, rule)
+    assert bad == 0, f"first mismatch at bits {first:#010x}"
+
+
+def _err(L):
+    return L.stm_last_error().decode()
+
+
+def test_invalid_arguments_are_rejected_without_a_gpu(L):
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    assert L.stm_nf4_quantize(p, 0, 128, 100, 0, p, p, None) == -1
+    assert "blocksize" in _err(L)
+    assert L.stm_nf4_quantize(p, 9, 128, 64, 0, p, p, None) == -1
+    assert L.stm_nf4_quantize(p, 0, 128, 64, 5, p, p, None) == -1
+    assert L.stm_nf4_quantize(None, 0, 128, 64, 0, p, p, None) == -1
+    assert L.stm_nf4_quantize(None, 0, 0, 64, 0, None, None, None) == 0  # empty input is a no-op
+    assert L.stm_nf4_dequantize(p, p, -1, 64, p, 0, None) == -1
+    assert L.stm_nf4_dequantize(p, p, 16, 64, p, 7, None) == -1
+    assert L.stm_nf4_dequantize(None, None, 0, 64, None, 0, None) == 0
+    # K not a multiple of 64 -> unsupported
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 100, 64, 1, None) == -2
+    assert "multiple of 64" in _err(L)
+    # fp32 GEMM is not a thing
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 64, 64, 2, None) == -1
+    # bad LoRA rank
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, p, p, 8, p, 4, 8, 64, 64, 1, None) == -1
+    # backward needs N % 64 == 0
+    assert L.stm_nf4_gemm_bwd_dx(p, p, p, None, None, 0, p, 4, 40, 64, 64, 1, None) == -2
+    # misaligned pointer
+    assert L.stm_nf4_gemm_fwd(p + 2, p, p, None, None, None, 0, p, 4, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, None, 4, 16, p, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, p, 0, 16, p, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_decision_boundaries(3, p) == -1
+
+
+def test_python_wrapper_raises_value_error_on_bad_arguments():
+    import torch
+    from stratum_amd import functional as F
+    with pytest.raises(NotImplementedError):
+        F.quantize_4bit(torch.zeros(64, 64), quant_type="fp4")
+    with pytest.raises(ValueError):
+        F.quantize_4bit(torch.zeros(64, 64), blocksize=100)
+    with pytest.raises(NotImplementedError):
+        F.quantize_4bit(torch.zeros(64, 64), compress_statistics=True)
+    with pytest.raises(RuntimeError):
+        F.dequantize_4bit(torch.zeros(32, 1, dtype=torch.uint8), absmax=torch.ones(1), shape=(8, 8))

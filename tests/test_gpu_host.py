@@ -1,0 +1,201 @@
+"""GPU tests of the host layer: the NF4 staging lifecycle (prepare_nf4 ->
+ensure_weights -> free_weights, prefetch, cache) and NF4Linear / NF4LoRALinear
+autograd, checked against the oracle (bit-exact weights) and fp32 references."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import c_oracle as C
+from oracle import nf4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def seeded(shape, seed, std, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+
+def bits16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def oracle_weight(w, dtype, device):
+    """Oracle dequantization of an fp16 weight to *dtype*, as a float32 tensor."""
+    p, a = C.quantize(bits16(w), O.DT_F16, 64, "argmin")
+    tag = O.DT_F16 if dtype == torch.float16 else O.DT_BF16
+    bits = C.dequantize(p, a, w.numel(), 64, tag).view(np.int16).reshape(w.shape)
+    return torch.from_numpy(bits).view(dtype).float().to(device)
+
+
+def oracle_dequant_bits(w, bs=64):
+    x = bits16(w)
+    p, a = C.quantize(x, O.DT_F16 if w.dtype == torch.float16 else O.DT_BF16, bs, "argmin")
+    return C.dequantize(p, a, w.numel(), bs, O.DT_F16 if w.dtype == torch.float16 else O.DT_BF16)
+
+
+class _Block(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.q_proj = nn.Linear(256, 512, bias=False, dtype=torch.float16)
+        self.experts = nn.Parameter(seeded((4, 128, 64), 3, 0.02, torch.float16), requires_grad=False)
+        self.norm = nn.LayerNorm(256, dtype=torch.float16).requires_grad_(False)
+        self.register_buffer("running", torch.zeros(8))
+        with torch.no_grad():
+            self.q_proj.weight.copy_(seeded((512, 256), 1, 0.02, torch.float16))
+        self.q_proj.weight.requires_grad_(False)
+
+
+def test_prepare_ensure_free_lifecycle_is_bit_exact(cuda):
+    from stratum_amd.upload import NF4_ATTR, ensure_weights, free_weights, prepare_nf4
+    m = _Block()
+    w_q = m.q_proj.weight.detach().clone()
+    w_e = m.experts.detach().clone()
+    stats = prepare_nf4(m, min_numel=4096, verbose=False)
+    assert stats.tensors == 2
+    assert m.q_proj.weight.numel() == 0 and m.experts.numel() == 0
+    pay = getattr(m.experts, NF4_ATTR)
+    assert pay.shape == (4, 128, 64) and pay.quantized.is_pinned() and pay.quantized.shape == (4 * 128 * 64 // 2, 1)
+    n = ensure_weights(m, 0)
+    assert n >= 2
+    assert m.q_proj.weight.device.type == "cuda" and m.q_proj.weight.dtype == torch.float16
+    np.testing.assert_array_equal(bits16(m.q_proj.weight).ravel(), oracle_dequant_bits(w_q))
+    np.testing.assert_array_equal(bits16(m.experts).ravel(), oracle_dequant_bits(w_e.reshape(-1, 64)))
+    assert m.experts.shape == (4, 128, 64)
+    assert m.running.device.type == "cuda" and m.norm.weight.device.type == "cuda"
+    assert ensure_weights(m, 0) == 0  # everything already materialised
+    assert free_weights(m) == 2
+    assert m.q_proj.weight.numel() == 0
+    assert ensure_weights(m, 0) == 2  # second step re-materialises from the payload
+    np.testing.assert_array_equal(bits16(m.q_proj.weight).ravel(), oracle_dequant_bits(w_q))
+
+
+def test_side_stream_upload_with_fence(cuda):
+    """DeviceStage pattern: ensure_weights on a param stream, event, default stream waits."""
+    from stratum_amd.upload import ensure_weights, free_weights, prepare_nf4
+    layers = [nn.Linear(512, 512, bias=False, dtype=torch.float16) for _ in range(3)]
+    ref = []
+    for i, l in enumerate(layers):
+        with torch.no_grad():
+            l.weight.copy_(seeded((512, 512), 10 + i, 0.02, torch.float16))
+        l.weight.requires_grad_(False)
+        ref.append(oracle_dequant_bits(l.weight.detach().clone()))
+        prepare_nf4(l, verbose=False)
+    x = seeded((64, 512), 99, 1.0, torch.float16).to(cuda)
+    param_stream = torch.cuda.Stream()
+    default = torch.cuda.default_stream()
+    outs = []
+    for step in range(2):
+        fences = []
+        for l in layers:
+            with torch.cuda.stream(param_stream):
+                ensure_weights(l, 0)
+            ev = torch.cuda.Event()
+            ev.record(param_stream)
+            fences.append(ev)
+        h = x
+        for l, ev in zip(layers, fences):
+            default.wait_event(ev)
+            h = l(h)
+        outs.append(h.float().cpu())
+        for i, l in enumerate(layers):
+            np.testing.assert_array_equal(bits16(l.weight).ravel(), ref[i])
+            free_weights(l)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_prefetch_then_finalize(cuda):
+    from stratum_amd.upload import ensure_prefetched_weights, free_weights, prefetch_weights, prepare_nf4
+    m = _Block()
+    w_q = m.q_proj.weight.detach().clone()
+    prepare_nf4(m, verbose=False)
+    pf = prefetch_weights(m, 0)
+    assert len(pf.entries) == 2 and pf.event is not None
+    assert m.q_proj.weight.numel() == 0  # parameter data untouched until finalize
+    n = ensure_prefetched_weights(m, 0, pf)
+    assert n >= 2
+    np.testing.assert_array_equal(bits16(m.q_proj.weight).ravel(), oracle_dequant_bits(w_q))
+    with pytest.raises(ValueError):
+        ensure_prefetched_weights(m, 1, pf)
+    free_weights(m)
+    assert prefetch_weights(nn.Linear(4, 4), 0).entries == []
+
+
+def test_cache_roundtrip_and_from_cache(cuda, tmp_path):
+    from stratum_amd.upload import NF4_ATTR, ensure_weights, prepare_nf4, prepare_nf4_from_cache
+    m1 = _Block()
+    w_q = m1.q_proj.weight.detach().clone()
+    s1 = prepare_nf4(m1, cache_dir=tmp_path, verbose=False)
+    assert s1.cache_misses == 2 and s1.cache_writes == 2
+    m2 = _Block()
+    s2 = prepare_nf4(m2, cache_dir=tmp_path, verbose=False)
+    assert s2.cache_hits == 2 and s2.cache_writes == 0
+    p1, p2 = getattr(m1.q_proj.weight, NF4_ATTR), getattr(m2.q_proj.weight, NF4_ATTR)
+    assert torch.equal(p1.quantized, p2.quantized) and torch.equal(p1.absmax, p2.absmax)
+    m3 = _Block()
+    for prm in (m3.q_proj.weight, m3.experts):  # weights never materialised on the host
+        prm.data = torch.empty(prm.shape, dtype=prm.dtype, device="meta")
+    s3 = prepare_nf4_from_cache(m3, tmp_path, verbose=False)
+    assert s3 is not None and s3.tensors == 2 and s3.cache_hits == 2
+    assert m3.q_proj.weight.device.type == "cpu" and m3.q_proj.weight.numel() == 0
+    ensure_weights(m3, 0)
+    np.testing.assert_array_equal(bits16(m3.q_proj.weight).ravel(), oracle_dequant_bits(w_q))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_nf4_linear_forward_backward(cuda, dtype):
+    from stratum_amd.functional import quantize_4bit
+    from stratum_amd.nf4_linear import NF4Linear
+    N, K, M = 384, 256, 200
+    w = seeded((N, K), 5, 0.02, torch.float16)
+    q, st = quantize_4bit(w.to(cuda))
+    st.dtype = dtype
+    bias = seeded((N,), 6, 0.1, dtype).to(cuda)
+    lin = NF4Linear(q, st, bias=bias)
+    assert lin.in_features == K and lin.out_features == N
+    wq = oracle_weight(w, dtype, cuda)
+    x = seeded((4, M // 4, K), 7, 1.0, dtype).to(cuda).requires_grad_(True)
+    y = lin(x)
+    xr = x.detach().float().requires_grad_(True)
+    yr = xr @ wq.t().contiguous() + bias.float()
+    tol = 1e-2 if dtype == torch.bfloat16 else 5e-3
+    assert ((y.float() - yr).norm() / yr.norm()).item() <= tol
+    g = seeded(tuple(y.shape), 8, 1.0, dtype).to(cuda)
+    y.backward(g)
+    yr.backward(g.float())
+    assert ((x.grad.float() - xr.grad).norm() / xr.grad.norm()).item() <= tol
+
+
+def test_nf4_lora_linear_gradients(cuda):
+    from stratum_amd.functional import quantize_4bit
+    from stratum_amd.nf4_linear import NF4LoRALinear
+    dtype = torch.bfloat16
+    N, K, M, r = 512, 256, 160, 16
+    w = seeded((N, K), 15, 0.02, torch.float16)
+    q, st = quantize_4bit(w.to(cuda))
+    st.dtype = dtype
+    lin = NF4LoRALinear(q, st, r=r, lora_alpha=32.0)
+    with torch.no_grad():
+        lin.lora_A.copy_(seeded((r, K), 16, 0.05, dtype))
+        lin.lora_B.copy_(seeded((N, r), 17, 0.05, dtype))
+    wq = oracle_weight(w, dtype, cuda)
+    x = seeded((M, K), 18, 1.0, dtype).to(cuda).requires_grad_(True)
+    y = lin(x)
+    g = seeded((M, N), 19, 1.0, dtype).to(cuda)
+    y.backward(g)
+    A = lin.lora_A.detach().float().requires_grad_(True)
+    B = lin.lora_B.detach().float().requires_grad_(True)
+    xr = x.detach().float().requires_grad_(True)
+    yr = xr @ wq.t().contiguous() + (xr @ A.t().contiguous()) @ B.t().contiguous() * lin.scaling
+    yr.backward(g.float())
+
+    def rel(a_, b_):
+        return ((a_.float() - b_).norm() / b_.norm()).item()
+
+    assert rel(y, yr) <= 1e-2
+    assert rel(x.grad, xr.grad) <= 1e-2
+    assert rel(lin.lora_A.grad, A.grad) <= 2e-2
+    assert rel(lin.lora_B.grad, B.grad) <= 2e-2

@@ -1,0 +1,265 @@
+"""GPU parity of the HIP kernels against the CPU oracle.
+
+Bar: quantize (packed codes + absmax) and dequantize are bit-exact; fused GEMMs
+are within a relative Frobenius error of 1e-2 (bf16) / 5e-3 (fp16) of an fp32
+matmul on the oracle-dequantized weight (the tolerances the north-star states).
+"""
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle as C
+from oracle import nf4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-3}
+TAG = {torch.float16: O.DT_F16, torch.bfloat16: O.DT_BF16, torch.float32: O.DT_F32}
+
+
+def seeded(shape, seed, std, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+
+def host_bits(t):
+    """CPU numpy view of a tensor's raw bits (uint16 for 16-bit, uint32 for fp32)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float32:
+        return t.view(torch.int32).numpy().view(np.uint32)
+    return t.numpy()
+
+
+def oracle_quant(x, bs, rule="argmin"):
+    return C.quantize(host_bits(x) if x.dtype != torch.float32 else x.numpy(), TAG[x.dtype], bs, rule)
+
+
+def oracle_deq_tensor(packed, absmax, shape, bs, dtype):
+    n = int(np.prod(shape))
+    bits = C.dequantize(packed, absmax, n, bs, TAG[dtype])
+    if dtype == torch.float32:
+        return torch.from_numpy(bits.view(np.float32).reshape(shape))
+    return torch.from_numpy(bits.view(np.int16).reshape(shape)).view(dtype)
+
+
+# -------------------------------------------------------------- quantize
+@pytest.mark.parametrize("rule", ["argmin", "threshold"])
+@pytest.mark.parametrize("dtype,shape,bs", [
+    (torch.float16, (5632, 2048), 64),      # TinyLlama gate_proj, the CPU-runnable reference case
+    (torch.bfloat16, (1024, 1024), 64),
+    (torch.float32, (256, 1024), 64),
+    (torch.float16, (64, 1024), 128),
+    (torch.float16, (32, 2048), 256),
+    (torch.bfloat16, (16, 4096), 512),
+    (torch.float16, (8, 4096), 1024),
+    (torch.float32, (4, 8192), 4096),
+    (torch.float16, (1001,), 64),           # odd length, partial last block
+    (torch.float16, (3, 100), 64),          # n % 8 != 0
+])
+def test_quantize_bit_exact(cuda, rule, dtype, shape, bs):
+    from stratum_amd.functional import quantize_4bit
+    x = seeded(shape, 100 + bs, 0.02 if dtype != torch.float32 else 1.0, dtype)
+    packed, state = quantize_4bit(x.to(cuda), blocksize=bs, rounding=rule)
+    ref_p, ref_a = oracle_quant(x, bs, rule)
+    assert packed.shape == ((x.numel() + 1) // 2, 1) and packed.dtype == torch.uint8
+    assert state.absmax.dtype == torch.float32 and state.shape == x.shape and state.dtype == dtype
+    np.testing.assert_array_equal(host_bits(state.absmax), ref_a.view(np.uint32))
+    np.testing.assert_array_equal(packed.cpu().numpy().ravel(), ref_p)
+
+
+def test_quantize_unaligned_input_and_cpu_input(cuda):
+    from stratum_amd import _lib
+    from stratum_amd.functional import quantize_4bit
+    base = seeded((4097,), 9, 0.02, torch.float16)
+    x = base[1:].contiguous()
+    rp, ra = oracle_quant(x, 64)
+    # a pointer 2 bytes past an allocation takes the library's unaligned path
+    xg = base.to(cuda)[1:]
+    p = torch.empty(2048, dtype=torch.uint8, device=cuda)
+    a = torch.empty(64, dtype=torch.float32, device=cuda)
+    rc = _lib.lib().stm_nf4_quantize(xg.data_ptr(), _lib.STM_F16, 4096, 64, _lib.STM_NF4_ARGMIN, p.data_ptr(),
+                                     a.data_ptr(), _lib.stream_handle(cuda))
+    assert rc == 0
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
+    np.testing.assert_array_equal(host_bits(a), ra.view(np.uint32))
+    # a CPU input is quantized on the GPU and returned on the CPU, like bitsandbytes
+    p2, s2 = quantize_4bit(x, blocksize=64)
+    assert p2.device.type == "cpu" and s2.absmax.device.type == "cpu"
+    np.testing.assert_array_equal(p2.numpy().ravel(), rp)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))))
+def test_kernels_reproduce_golden_fixtures(cuda, path):
+    from stratum_amd.functional import dequantize_4bit, quantize_4bit
+    f = np.load(path)
+    x, tag, bs = f["x"], int(f["dtype_tag"]), int(f["blocksize"])
+    if tag == O.DT_F16:
+        xt = torch.from_numpy(x)
+    elif tag == O.DT_BF16:
+        xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x)
+    for rule in ("argmin", "threshold"):
+        p, s = quantize_4bit(xt.to(cuda), blocksize=bs, rounding=rule)
+        np.testing.assert_array_equal(p.cpu().numpy().ravel(), f[f"packed_{rule}"])
+        np.testing.assert_array_equal(host_bits(s.absmax), f[f"absmax_{rule}"].view(np.uint32))
+    n = x.size
+    q = torch.from_numpy(f["packed_argmin"]).to(cuda)
+    a = torch.from_numpy(f["absmax_argmin"]).to(cuda)
+    for dt, key in ((torch.float16, "deq_f16"), (torch.bfloat16, "deq_bf16"), (torch.float32, "deq_f32")):
+        out = dequantize_4bit(q, absmax=a, shape=(n,), blocksize=bs, dtype=dt)
+        want = f[key].view(np.uint32) if dt == torch.float32 else f[key]
+        np.testing.assert_array_equal(host_bits(out), want)
+
+
+# ------------------------------------------------------------ dequantize
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape,bs", [((5632, 2048), 64), ((14336, 4096), 64), ((128, 4096), 4096),
+                                      ((1001,), 64), ((7, 9), 64)])
+def test_dequantize_bit_exact(cuda, out_dtype, shape, bs):
+    from stratum_amd.functional import dequantize_4bit
+    x = seeded(shape, 7, 0.02, torch.float16)
+    rp, ra = oracle_quant(x, bs)
+    q = torch.from_numpy(rp).reshape(-1, 1).to(cuda)
+    a = torch.from_numpy(ra).to(cuda)
+    out = dequantize_4bit(q, absmax=a, shape=shape, blocksize=bs, dtype=out_dtype)
+    assert out.shape == torch.Size(shape) and out.dtype == out_dtype and out.is_contiguous()
+    want = C.dequantize(rp, ra, x.numel(), bs, TAG[out_dtype])
+    np.testing.assert_array_equal(host_bits(out).ravel(), want.view(np.uint32) if out_dtype == torch.float32 else want)
+
+
+def test_dequantize_into_misaligned_out(cuda):
+    from stratum_amd.functional import dequantize_4bit
+    x = seeded((4096,), 8, 0.02, torch.float16)
+    rp, ra = oracle_quant(x, 64)
+    buf = torch.empty(4097, dtype=torch.float16, device=cuda)
+    out = buf[1:]
+    dequantize_4bit(torch.from_numpy(rp).to(cuda), absmax=torch.from_numpy(ra).to(cuda), shape=(4096,),
+                    blocksize=64, dtype=torch.float16, out=out)
+    np.testing.assert_array_equal(host_bits(out), C.dequantize(rp, ra, 4096, 64, O.DT_F16))
+
+
+def test_all_zero_block_dequantizes_to_negative_zero(cuda):
+    from stratum_amd.functional import dequantize_4bit, quantize_4bit
+    x = torch.zeros(2, 64, dtype=torch.float16)
+    x[1, 3] = 0.5
+    p, s = quantize_4bit(x.to(cuda))
+    assert s.absmax[0].item() == 0.0
+    out = dequantize_4bit(p, s)
+    bits = host_bits(out)
+    assert np.all(bits[0] == 0x8000)  # code 0 (-1.0) * 0.0 = -0.0, as the reference computes it
+
+
+def test_roundtrip_is_idempotent_at_8b_mlp_size(cuda):
+    """quantize(dequantize(quantize(W))) == quantize(W) at the full [14336, 4096] size."""
+    from stratum_amd.functional import dequantize_4bit, quantize_4bit
+    w = seeded((14336, 4096), 42, 0.02, torch.float16).to(cuda)
+    p1, s1 = quantize_4bit(w)
+    d1 = dequantize_4bit(p1, s1)
+    p2, s2 = quantize_4bit(d1)
+    assert torch.equal(p1, p2)
+    assert torch.equal(s1.absmax, s2.absmax)
+
+
+# ------------------------------------------------------------- fused GEMM
+def _rel(y, ref):
+    y = y.float()
+    return ((y - ref).norm() / ref.norm()).item()
+
+
+def _nf4_weight(N, K, seed, bs=64, src=torch.float16):
+    w = seeded((N, K), seed, 0.02, src)
+    rp, ra = oracle_quant(w, bs)
+    return rp, ra
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,bias,rank", [
+    (1, 128, 64, False, 0), (37, 200, 192, True, 0), (128, 128, 128, False, 16), (300, 520, 576, True, 16),
+    (4096, 2048, 1024, False, 0), (512, 14336, 4096, False, 16), (129, 1024, 3072, True, 32),
+])
+def test_gemm_fwd_matches_fp32_reference(cuda, dtype, M, N, K, bias, rank):
+    from stratum_amd.functional import nf4_gemm_fwd
+    rp, ra = _nf4_weight(N, K, M + N + K)
+    wq = oracle_deq_tensor(rp, ra, (N, K), 64, dtype).to(cuda)
+    x = seeded((M, K), 1, 1.0, dtype).to(cuda)
+    b = seeded((N,), 2, 0.1, dtype).to(cuda) if bias else None
+    t = seeded((M, rank), 3, 0.5, dtype).to(cuda) if rank else None
+    lb = seeded((N, rank), 4, 0.01, dtype).to(cuda) if rank else None
+    y = nf4_gemm_fwd(x, torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda), (N, K), 64, bias=b,
+                     lora_t=t, lora_b=lb)
+    ref = x.float() @ wq.float().t().contiguous()
+    if bias:
+        ref = ref + b.float()
+    if rank:
+        ref = ref + t.float() @ lb.float().t().contiguous()
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel(y, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,rank", [
+    (1, 64, 64, 0), (37, 192, 128, 0), (300, 576, 512, 16), (4096, 1024, 2048, 0), (512, 14336, 4096, 16),
+    (129, 3072, 1024, 32),
+])
+def test_gemm_bwd_dx_matches_fp32_reference(cuda, dtype, M, N, K, rank):
+    from stratum_amd.functional import nf4_gemm_bwd_dx
+    rp, ra = _nf4_weight(N, K, M * 3 + N + K)
+    wq = oracle_deq_tensor(rp, ra, (N, K), 64, dtype).to(cuda)
+    dy = seeded((M, N), 5, 1.0, dtype).to(cuda)
+    u = seeded((M, rank), 6, 0.5, dtype).to(cuda) if rank else None
+    at = seeded((K, rank), 7, 0.01, dtype).to(cuda) if rank else None
+    dx = nf4_gemm_bwd_dx(dy, torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda), (N, K), 64,
+                         lora_u=u, lora_at=at)
+    ref = dy.float() @ wq.float()
+    if rank:
+        ref = ref + u.float() @ at.float().t().contiguous()
+    assert dx.shape == (M, K) and dx.dtype == dtype
+    assert _rel(dx, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16])
+def test_gemm_full_lora_step_shape(cuda, dtype):
+    """W [14336, 4096], X [8192, 4096]: forward and input gradient at full size."""
+    from stratum_amd.functional import nf4_gemm_bwd_dx, nf4_gemm_fwd
+    N, K, M = 14336, 4096, 8192
+    rp, ra = _nf4_weight(N, K, 55)
+    wq = oracle_deq_tensor(rp, ra, (N, K), 64, dtype).to(cuda).float()
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    x = seeded((M, K), 1, 1.0, dtype).to(cuda)
+    y = nf4_gemm_fwd(x, q, a, (N, K), 64)
+    assert _rel(y, x.float() @ wq.t().contiguous()) <= TOL[dtype]
+    del y
+    dy = seeded((M, N), 2, 1.0, dtype).to(cuda)
+    dx = nf4_gemm_bwd_dx(dy, q, a, (N, K), 64)
+    assert _rel(dx, dy.float() @ wq) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_gemm_matches_per_expert_reference(cuda, dtype):
+    from stratum_amd.functional import nf4_grouped_gemm
+    E, N, K = 8, 256, 192
+    w = seeded((E, N, K), 77, 0.02, torch.float16)
+    rp, ra = oracle_quant(w.reshape(-1, K), 64)
+    wq = oracle_deq_tensor(rp, ra, (E, N, K), 64, dtype).to(cuda).float()
+    counts = [0, 5, 130, 64, 1, 0, 257, 33]
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    Mt = int(off[-1])
+    x = seeded((Mt, K), 8, 1.0, dtype).to(cuda)
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    y = nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), 64)
+    dy = seeded((Mt, N), 9, 1.0, dtype).to(cuda)
+    dx = nf4_grouped_gemm(dy, q, a, off.to(cuda), (N, K), 64, backward=True)
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        assert _rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype]
+        assert _rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype]
