@@ -3,33 +3,60 @@
 // forward  Y[M, N]  = X[M, K] . W[N, K]^T  (+ bias) (+ T . L^T)
 // backward dX[M, K] = dY[M, N] . W[N, K]            (+ U . At^T)
 //
-// Work-group tile 128 x 128, 4 waves in a 2 x 2 grid, each wave 64 x 64 as
-// 2 x 2 v_mfma_f32_32x32x16 tiles; the reduction advances 64 at a time (one
-// NF4 block of 64 when blocksize = 64). Per step the activation tile is copied
-// to LDS and the packed W tile is dequantized (level table in LDS, fp32
-// product with the block absmax, one round-to-nearest-even conversion: the
-// same values the dequantize kernel writes) straight into LDS, so every
-// dequantized element is reused by 128 rows of activations. LDS rows are
-// 64 halfs (128 B = eight 16-byte chunks); chunk c of row r lives at
-// c ^ (r & 7), which makes both the 16-byte fragment reads of the MFMA loop
-// and the 16-byte tile writes bank-conflict free. Two LDS buffers: the global
-// loads of step k+1 are in flight while the MFMAs of step k run.
+// Work-group tile BM x BN (activation rows x output columns), WM x WN waves,
+// each wave (BM/WM) x (BN/WN) as a grid of v_mfma_f32_32x32x16 tiles; the
+// reduction advances 64 per step (one NF4 block when blocksize = 64).
 //
-// MFMA operand layout (v_mfma_f32_32x32x16_{bf16,f16}): lane l supplies
-// A[l % 32][8 (l / 32) .. +8] and B[8 (l / 32) .. +8][l % 32]; the 16 results of
-// lane l are C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32], v = 0..15.
+// Per step and LDS buffer:
+//  * the activation tile (BM rows x 64) is copied global -> LDS with
+//    global_load_lds_dwordx4 (no VGPR round trip): lane l of a wave writes the
+//    16-byte LDS slot l of a 1 KB run, so the bank swizzle below is applied on the
+//    global-address side (each lane fetches the chunk that belongs in its slot);
+//  * the packed weight tile is loaded to VGPRs and dequantized with a 256-entry
+//    (level_hi, level_lo) table in LDS, one fp32 product with the block absmax and
+//    one round-to-nearest-even conversion -- the values the dequantize kernel
+//    writes -- straight into LDS. Forward stores W rows [n][k]; backward stores
+//    the transpose [k][n] (an 8 x 8 register transpose per thread) so that the
+//    MFMA operand (8 consecutive reduction indices per lane) is one 16-byte read.
+// LDS rows are 64 halfs = eight 16-byte chunks; chunk c of row r sits at
+// c ^ ((r >> 1) & 7), so the 16 lanes of one 16-byte LDS pass (16 consecutive
+// rows, one logical chunk) land on 16 different 16-byte bank groups.
+// Two buffers: the loads of step k+1 are in flight while step k's MFMAs run.
+//
+// The MFMA computes the transposed tile (W-side operand as A, activation as B),
+// so each lane's accumulators hold 4 consecutive output columns of one row and
+// the epilogue writes 8-byte runs.
+//
+// MFMA layout (v_mfma_f32_32x32x16): lane l supplies A[l % 32][k-group l / 32]
+// and B[k-group l / 32][l % 32] (8 halfs each; any k order common to A and B
+// gives the same product); result v of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
 #include <type_traits>
 
 #include "nf4_kernels.h"
+
+// Tile shapes (measured best on MI355X at M = 8192, N = 14336, K = 4096):
+// forward 256 x 256 with 8 waves (4 x 2), input gradient 256 x 256 with 4 waves.
+#ifndef STM_FWD_BM
+#define STM_FWD_BM 256
+#define STM_FWD_BN 256
+#define STM_FWD_WM 4
+#define STM_FWD_WN 2
+#endif
+#ifndef STM_BWD_BM
+#define STM_BWD_BM 256
+#define STM_BWD_BN 256
+#define STM_BWD_WM 2
+#define STM_BWD_WN 2
+#endif
+#ifndef STM_GROUP_M
+#define STM_GROUP_M 8
+#endif
 
 namespace stm {
 
 namespace {
 
-constexpr int BM = 128;   // rows of the activation / output tile
-constexpr int BN = 128;   // output columns per tile
-constexpr int BK = 64;    // reduction step
-constexpr int NT = 256;   // threads
+constexpr int BK = 64;  // reduction step
 
 template <typename Tr>
 __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
@@ -41,9 +68,38 @@ __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f
                                                       0, 0, 0);
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+#ifndef STM_SWZ
+#define STM_SWZ 1
+#endif
+__device__ __forceinline__ int swz_key(int row) { return STM_SWZ ? ((row >> 1) & 7) : (row & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
 
-// Group bookkeeping: expert e owns rows [row0, row0 + rows) of a/out and the
+typedef __attribute__((address_space(3))) uint4 lds_uint4;
+
+__device__ __forceinline__ uint32_t lds_offset(const uint4* p) {
+    return (uint32_t)(size_t)((const lds_uint4*)(p));
+}
+
+// 16 bytes global -> LDS for every lane of the wave; the LDS destination is
+// lds_base + 16 * lane (lds_base wave-uniform, in M0). Issued as inline asm so
+// the compiler does not treat every later LDS read as dependent on it (it
+// cannot tell the two LDS buffers apart and would wait for the copy before the
+// MFMA operand reads of the other buffer); completion is awaited explicitly
+// with wait_vmem() before the barrier that publishes the buffer.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
+                     : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima). Emitted through the
+// builtin so the compiler's own wait-count bookkeeping sees it and inserts no
+// further waits for the weight registers loaded before it.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Expert e owns rows [row0, row0 + rows) of the activations/outputs and the
 // e-th [N, K] slice of the packed weight.
 struct Group {
     int64_t row0, rows;
@@ -66,308 +122,484 @@ __device__ __forceinline__ Group group_of(const GemmArgs& g, int e) {
     return r;
 }
 
-// One packed byte -> two dequantized 16-bit values (even element in the low half).
-template <typename Tr>
-__device__ __forceinline__ uint32_t deq2(const float2* __restrict__ lut, uint32_t byte, float a) {
-    const float2 c = lut[byte];
-    return Tr::pack2(opaque(c.x * a), opaque(c.y * a));
+// Tile order: work-groups are dispatched round-robin over the 8 XCDs, so ids
+// i, i + 8, i + 16, ... share an L2. Give each XCD a contiguous run of tiles and
+// walk them GROUP_M activation tiles at a time so concurrently running tiles on
+// one XCD reuse the same activation rows and weight rows.
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
+    const int64_t T = ntm * ntn;
+    const int64_t T8 = (T / 8) * 8;
+    if (pid < T8) pid = (pid % 8) * (T / 8) + pid / 8;
+    const int64_t per_group = (int64_t)STM_GROUP_M * ntn;
+    const int64_t grp = pid / per_group;
+    const int64_t first = grp * STM_GROUP_M;
+    const int64_t gsize = (ntm - first) < STM_GROUP_M ? (ntm - first) : STM_GROUP_M;
+    const int64_t in = pid % per_group;
+    tm = first + in % gsize;
+    tn = in / gsize;
 }
 
-// Rank-R epilogue term: acc[i][j] += A_r[rows] . B_r[cols]^T, both operands
-// row-major with R contiguous (rows of the lora_x / lora_w matrices).
-template <typename Tr>
-__device__ __forceinline__ void lora_term(f32x16_t (&acc)[2][2], const uint16_t* __restrict__ ax, int64_t row_base,
-                                          int64_t rows_valid, const uint16_t* __restrict__ bw, int64_t col_base,
-                                          int64_t cols_valid, int R, int lane) {
-    for (int r0 = 0; r0 < R; r0 += 16) {
-        uint4 a[2], b[2];
+// Copy the activation tile rows [m0, m0 + BM) x [k0, k0 + 64) into LDS buffer
+// `dst` (BM x 8 chunks). Rows past the valid range re-read the last valid row:
+// they only feed output rows that are never stored.
+template <int BM, int NW>
+__device__ __forceinline__ void stage_act(const uint16_t* __restrict__ src, int64_t ld, int64_t m0, int64_t rows,
+                                          int64_t k0, const uint4* dst, int wave, int lane) {
+    constexpr int XI = BM / (8 * NW);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int64_t row = row_base + i * 32 + (lane & 31);
-            a[i] = make_uint4(0, 0, 0, 0);
-            if (row < rows_valid) a[i] = *reinterpret_cast<const uint4*>(ax + row * R + r0 + 8 * (lane >> 5));
-            const int64_t col = col_base + i * 32 + (lane & 31);
-            b[i] = make_uint4(0, 0, 0, 0);
-            if (col < cols_valid) b[i] = *reinterpret_cast<const uint4*>(bw + col * R + r0 + 8 * (lane >> 5));
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = mfma<Tr>(a[i], b[j], acc[i][j]);
+    for (int i = 0; i < XI; ++i) {
+        const int r0 = (wave * XI + i) * 8;
+        const int r = r0 + (lane >> 3);
+        const int c = (lane & 7) ^ swz_key(r);
+        int64_t row = m0 + r;
+        row = row < rows ? row : rows - 1;
+        dma16(src + row * ld + k0 + c * 8, __builtin_amdgcn_readfirstlane(lds_offset(dst + r0 * 8)));
     }
 }
 
-template <typename Tr>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[2][2], uint16_t* __restrict__ out, int64_t ld,
-                                           int64_t row_base, int64_t rows_valid, int64_t col_base, int64_t cols_valid,
+// Level table: entry (byte b, copy c) = (level[b >> 4], level[b & 15]) at
+// index 16 b + c. Lane l reads copy l % 16, so the 16 lanes of one LDS pass of
+// a 64-bit read always hit 16 different bank pairs (a single shared copy makes
+// random byte values collide on banks several times per read).
+constexpr int LUT_COPIES = 16;
+
+template <int NT>
+__device__ __forceinline__ void fill_lut(float2* lut, int tid) {
+    for (int t = tid; t < 256 * LUT_COPIES; t += NT) {
+        const int b = t / LUT_COPIES;
+        lut[t] = make_float2(kLevelsDev[b >> 4], kLevelsDev[b & 15]);
+    }
+}
+
+template <int FA, int FB>
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[FA][FB]) {
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+}
+
+// Rank-R term: acc[i][j] += Wside[rows] . Xside[cols]^T, both row-major with R contiguous.
+template <typename Tr, int FA, int FB>
+__device__ __forceinline__ void lora_term(f32x16_t (&acc)[FA][FB], const uint16_t* __restrict__ wside,
+                                          int64_t wrow_base, int64_t wrows, const uint16_t* __restrict__ xside,
+                                          int64_t xrow_base, int64_t xrows, int R, int lane) {
+    for (int r0 = 0; r0 < R; r0 += 16) {
+        uint4 a[FA], b[FB];
+#pragma unroll
+        for (int i = 0; i < FA; ++i) {
+            int64_t row = wrow_base + i * 32 + (lane & 31);
+            row = row < wrows ? row : wrows - 1;
+            a[i] = *reinterpret_cast<const uint4*>(wside + row * R + r0 + 8 * (lane >> 5));
+        }
+#pragma unroll
+        for (int j = 0; j < FB; ++j) {
+            int64_t row = xrow_base + j * 32 + (lane & 31);
+            row = row < xrows ? row : xrows - 1;
+            b[j] = *reinterpret_cast<const uint4*>(xside + row * R + r0 + 8 * (lane >> 5));
+        }
+#pragma unroll
+        for (int i = 0; i < FA; ++i)
+#pragma unroll
+            for (int j = 0; j < FB; ++j) acc[i][j] = mfma<Tr>(a[i], b[j], acc[i][j]);
+    }
+}
+
+// acc[i][j] holds C^T: rows = output columns (wcol_base + i*32 + ...), cols = output rows.
+template <typename Tr, int FA, int FB>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int64_t ld,
+                                           int64_t ocol_base, int64_t ocols, int64_t orow_base, int64_t orows,
                                            const uint16_t* __restrict__ bias, int lane) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int64_t col = col_base + j * 32 + (lane & 31);
-        if (col >= cols_valid) continue;
-        const float bv = bias ? Tr::to_f32(bias[col]) : 0.0f;
+    for (int j = 0; j < FB; ++j) {
+        const int64_t orow = orow_base + j * 32 + (lane & 31);
+        if (orow >= orows) continue;
+        uint16_t* dst = out + orow * ld;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FA; ++i) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = row_base + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (row < rows_valid) out[row * ld + col] = Tr::from_f32(acc[i][j][v] + bv);
+            for (int q = 0; q < 4; ++q) {
+                const int64_t col = ocol_base + i * 32 + 8 * q + 4 * (lane >> 5);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = acc[i][j][4 * q + e];
+                    if (bias && col + e < ocols) v[e] += Tr::to_f32(bias[col + e]);
+                }
+                if (col + 3 < ocols) {
+                    uint2 pk;
+                    pk.x = Tr::pack2(v[0], v[1]);
+                    pk.y = Tr::pack2(v[2], v[3]);
+                    *reinterpret_cast<uint2*>(dst + col) = pk;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < ocols) dst[col + e] = Tr::from_f32(v[e]);
+                }
             }
         }
     }
 }
 
-// ------------------------------------------------------------------ forward
-template <typename Tr>
-__global__ __launch_bounds__(NT) void k_gemm_fwd(GemmArgs g) {
-    __shared__ uint4 sA[2][BM * 8];
-    __shared__ uint4 sB[2][BN * 8];
-    __shared__ float2 lut[256];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    lut[tid] = make_float2(kLevelsDev[tid >> 4], kLevelsDev[tid & 15]);
-
-    const Group grp = group_of(g, blockIdx.y);
-    const int64_t ntn = (g.N + BN - 1) / BN;
-    const int64_t m0 = (int64_t)(blockIdx.x / ntn) * BM;
-    const int64_t n0 = (int64_t)(blockIdx.x % ntn) * BN;
-    if (m0 >= grp.rows) return;
-
-    const uint16_t* __restrict__ X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * g.K;
-    const int64_t K = g.K, N = g.N;
-    const int64_t kblocks = K / g.blocksize;
-    const int bshift = ilog2(g.blocksize);
-
-    // this thread's slice of the tiles
-    const int xa_row = tid >> 3, xa_chunk = tid & 7;     // + 32 * i, i = 0..3
-    const int wb_row = tid >> 1, wb_half = tid & 1;      // 16 packed bytes = 32 elements
-    const int64_t w_row = n0 + wb_row;
-    const bool w_ok = w_row < N;
-    const uint8_t* __restrict__ wp = grp.packed + w_row * (K / 2) + wb_half * 16;
-    const float* __restrict__ wa = grp.absmax + w_row * kblocks;
-
-    uint4 xr[4], wr;
-    float ar;
-    auto gload = [&](int kt) {
-        const int64_t k0 = (int64_t)kt * BK;
+// One 16-deep MFMA sub-step kk of a 64-deep step.
+template <typename Tr, int FA, int FB>
+__device__ __forceinline__ void mma_kk(f32x16_t (&acc)[FA][FB], const uint4* sw, int wrow0, const uint4* sx,
+                                       int xrow0, int lane, int kk) {
+    const int ch = kk * 2 + (lane >> 5);
+    uint4 a[FA], b[FB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t row = m0 + xa_row + 32 * i;
-            xr[i] = make_uint4(0, 0, 0, 0);
-            if (row < grp.rows) xr[i] = *reinterpret_cast<const uint4*>(X + row * K + k0 + xa_chunk * 8);
-        }
-        wr = make_uint4(0, 0, 0, 0);
-        ar = 0.0f;
-        if (w_ok) {
-            wr = *reinterpret_cast<const uint4*>(wp + k0 / 2);
-            ar = wa[k0 >> bshift];
-        }
-    };
-    auto lstore = [&](int buf) {
+    for (int i = 0; i < FA; ++i) a[i] = sw[swz(wrow0 + i * 32 + (lane & 31), ch)];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sA[buf][swz(xa_row + 32 * i, xa_chunk)] = xr[i];
-        const uint32_t w4[4] = {wr.x, wr.y, wr.z, wr.w};
+    for (int j = 0; j < FB; ++j) b[j] = sx[swz(xrow0 + j * 32 + (lane & 31), ch)];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {  // packed word c -> 8 elements -> one 16-byte chunk
-            uint4 o;
-            o.x = deq2<Tr>(lut, w4[c] & 0xFFu, ar);
-            o.y = deq2<Tr>(lut, (w4[c] >> 8) & 0xFFu, ar);
-            o.z = deq2<Tr>(lut, (w4[c] >> 16) & 0xFFu, ar);
-            o.w = deq2<Tr>(lut, w4[c] >> 24, ar);
-            sB[buf][swz(wb_row, wb_half * 4 + c)] = o;
-        }
-    };
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j) acc[i][j] = mfma<Tr>(a[i], b[j], acc[i][j]);
+}
 
-    f32x16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-    const int KT = (int)(K / BK);
-    gload(0);
-    __syncthreads();  // lut ready
-    lstore(0);
+// Shared main loop. Step s computes on buffers (s & 1) while the activation
+// tile of step s + 1 streams into the other LDS buffer, the weight tile of
+// step s + 1 (already in VGPRs) is dequantized into the other weight buffer,
+// and the packed weight tile of step s + 2 is fetched into VGPRs.
+//
+// The dequantization is software-pipelined against the MFMAs: it is cut into
+// four pieces; the level-table reads of piece i + 1 are issued before the
+// MFMAs of sub-step i and its arithmetic and LDS writes follow them, so the
+// VALU work and the LDS latency hide under the matrix pipe. Scheduling fences
+// keep the compiler from regrouping the pieces.
+//
+// Prefetch indices clamp at the last step, so the loop body has no branches;
+// the redundant copies at the end land in a buffer that is not read again.
+template <typename Tr, int BM, int BN, int WM, int WN, int FW, int FX, typename WS>
+__device__ __forceinline__ void run_pipeline(f32x16_t (&acc)[FW][FX], const uint16_t* act, int64_t ld, int64_t m0,
+                                             int64_t rows, int KT, uint4* sA0, uint4* sA1, uint4* sB0, uint4* sB1,
+                                             WS& ws, int wave, int lane) {
+    constexpr int NW = WM * WN;
+    const int wn = wave % WN, wm = wave / WN;
+    const int wrow0 = wn * (BN / WN), xrow0 = wm * (BM / WM);
+    typename WS::Regs w0, w1;
+
+    stage_act<BM, NW>(act, ld, m0, rows, 0, sA0, wave, lane);
+    ws.load(0, w0);
+    __syncthreads();  // level table ready
+    ws.store_all(w0, sB0);
+    ws.load(KT > 1 ? 1 : 0, w1);
+    wait_vmem();
     __syncthreads();
 
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
+    auto step = [&](int s, const uint4* sAc, const uint4* sBc, uint4* sAn, uint4* sBn, typename WS::Regs& wcur,
+                    typename WS::Regs& wnext) {
+        const int s1 = s + 1 < KT ? s + 1 : KT - 1;
+        const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+        stage_act<BM, NW>(act, ld, m0, rows, (int64_t)s1 * BK, sAn, wave, lane);
+        ws.load(s2, wnext);
+        typename WS::Pending pend[2];
+        ws.issue(wcur, 0, pend[0]);
+        sched_fence();
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
-            uint4 a[2], b[2];
-            const int ch = kk * 2 + (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = sA[cur][swz(wm * 64 + i * 32 + (lane & 31), ch)];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = sB[cur][swz(wn * 64 + j * 32 + (lane & 31), ch)];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma<Tr>(a[i], b[j], acc[i][j]);
+            mma_kk<Tr, FW, FX>(acc, sBc, wrow0, sAc, xrow0, lane, kk);
+            if (kk + 1 < BK / 16) ws.issue(wcur, kk + 1, pend[(kk + 1) & 1]);
+            ws.finish(wcur, kk, pend[kk & 1], sBn);
+            sched_fence();
         }
-        if (kt + 1 < KT) lstore(cur ^ 1);
+        ws.flush(sBn);
+        wait_vmem();
         __syncthreads();
+    };
+    int s = 0;
+    for (; s + 1 < KT; s += 2) {
+        step(s, sA0, sB0, sA1, sB1, w1, w0);
+        step(s + 1, sA1, sB1, sA0, sB0, w0, w1);
+    }
+    if (s < KT) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) mma_kk<Tr, FW, FX>(acc, sB0, wrow0, sA0, xrow0, lane, kk);
+    }
+}
+
+// ------------------------------------------------------------------ forward
+// Weight staging for the forward kernel: each thread owns WC 16-byte chunks
+// of packed codes per step (row cidx / 2, 32-element half cidx % 2, cidx =
+// tid + j * NT). Piece i of the dequantization is packed word i of every chunk
+// (8 elements -> one 16-byte LDS chunk).
+template <typename Tr, int WC, int NT>
+struct FwdStage {
+    struct Regs {
+        uint4 q[WC];
+        float a[WC];
+    };
+    struct Pending {
+        float2 c[WC][4];
+    };
+    const uint8_t* wp[WC];
+    const float* wa[WC];
+    const float2* lut;
+    int tid, bshift;
+
+    __device__ __forceinline__ void load(int s, Regs& w) const {
+        const int64_t k0 = (int64_t)s * BK;
+#pragma unroll
+        for (int j = 0; j < WC; ++j) {
+            w.q[j] = *reinterpret_cast<const uint4*>(wp[j] + k0 / 2);
+            w.a[j] = wa[j][k0 >> bshift];
+        }
+    }
+    __device__ __forceinline__ static uint32_t word(const uint4& q, int i) {
+        return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+    }
+    __device__ __forceinline__ void issue(const Regs& w, int i, Pending& p) const {
+#pragma unroll
+        for (int j = 0; j < WC; ++j) {
+            const uint32_t x = word(w.q[j], i);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) p.c[j][b] = lut[((x >> (8 * b)) & 0xFFu) * LUT_COPIES];
+        }
+    }
+    __device__ __forceinline__ void finish(const Regs& w, int i, const Pending& p, uint4* dst) const {
+#pragma unroll
+        for (int j = 0; j < WC; ++j) {
+            const int cidx = tid + j * NT;
+            const float a = w.a[j];
+            uint4 o;
+            o.x = Tr::pack2(opaque(p.c[j][0].x * a), opaque(p.c[j][0].y * a));
+            o.y = Tr::pack2(opaque(p.c[j][1].x * a), opaque(p.c[j][1].y * a));
+            o.z = Tr::pack2(opaque(p.c[j][2].x * a), opaque(p.c[j][2].y * a));
+            o.w = Tr::pack2(opaque(p.c[j][3].x * a), opaque(p.c[j][3].y * a));
+            dst[swz(cidx >> 1, (cidx & 1) * 4 + i)] = o;
+        }
+    }
+    __device__ __forceinline__ void flush(uint4*) const {}
+    __device__ __forceinline__ void store_all(const Regs& w, uint4* dst) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            Pending p;
+            issue(w, i, p);
+            finish(w, i, p, dst);
+        }
+    }
+};
+
+template <typename Tr, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
+    constexpr int NW = WM * WN, NT = NW * 64;
+    constexpr int FX = BM / WM / 32;  // activation-side fragments per wave (MFMA B operand)
+    constexpr int FW = BN / WN / 32;  // weight-side fragments per wave (MFMA A operand)
+    constexpr int WC = BN * 2 / NT;   // 16-byte packed weight chunks per thread per step
+    static_assert(BM % (8 * NW) == 0 && (BN * 2) % NT == 0, "tile / wave mismatch");
+    __shared__ float2 lut_all[256 * LUT_COPIES];
+    __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
+    __shared__ uint4 sB0[BN * 8], sB1[BN * 8];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    fill_lut<NT>(lut_all, tid);
+
+    const Group grp = group_of(g, blockIdx.y);
+    const int64_t K = g.K, N = g.N;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
+    int64_t tm, tn;
+    tile_coords(blockIdx.x, ntm, ntn, tm, tn);
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= grp.rows) return;
+
+    const uint16_t* __restrict__ X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K;
+    const int64_t kblocks = K / g.blocksize;
+
+    FwdStage<Tr, WC, NT> ws;
+    ws.lut = lut_all + (lane & (LUT_COPIES - 1));
+    ws.tid = tid;
+    ws.bshift = ilog2(g.blocksize);
+#pragma unroll
+    for (int j = 0; j < WC; ++j) {
+        const int cidx = tid + j * NT;
+        int64_t n = n0 + (cidx >> 1);
+        n = n < N ? n : N - 1;  // rows past N only feed columns that are never stored
+        ws.wp[j] = grp.packed + n * (K / 2) + (cidx & 1) * 16;
+        ws.wa[j] = grp.absmax + n * kblocks;
     }
 
-    const int64_t row_base = m0 + wm * 64, col_base = n0 + wn * 64;
+    f32x16_t acc[FW][FX];
+    zero_acc(acc);
+    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, X, K, m0, grp.rows, (int)(K / BK), sA0, sA1, sB0, sB1, ws, wave,
+                                             lane);
+
+    const int64_t col_base = n0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
     if (g.lora_rank > 0)
-        lora_term<Tr>(acc, reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base, grp.rows,
-                      reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N, g.lora_rank, lane);
-    store_tile<Tr>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, row_base, grp.rows, col_base, N,
-                   reinterpret_cast<const uint16_t*>(g.bias), lane);
+        lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
+                              reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
+                              grp.rows, g.lora_rank, lane);
+    store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, col_base, N, row_base, grp.rows,
+                           reinterpret_cast<const uint16_t*>(g.bias), lane);
 }
 
 // ----------------------------------------------------------------- backward
-// dX[m, k] = sum_n dY[m, n] W[n, k]: the W tile (64 rows n x 128 columns k) is
-// dequantized transposed into LDS as [k][n] so the MFMA B operand (8
-// consecutive n per lane) is one 16-byte read.
-template <typename Tr>
-__global__ __launch_bounds__(NT) void k_gemm_bwd(GemmArgs g) {
-    constexpr int BKO = 128;  // output columns (k) per tile
-    constexpr int BR = 64;    // reduction step over n
-    __shared__ uint4 sA[2][BM * 8];
-    __shared__ uint4 sB[2][BKO * 8];
-    __shared__ float2 lut[256];
+// dX[m, k] = sum_n dY[m, n] W[n, k]; the tile covers BM rows of dY/dX and BN
+// output columns k. Each step reduces over 64 rows n of W; every thread
+// dequantizes an 8 (n) x KB (k) block of the W slice and writes it transposed
+// (KB columns of 8 consecutive n = one 16-byte chunk each). Piece p of the
+// dequantization is the row pair (2p, 2p + 1); the transposed chunks are
+// written once all four pairs are done.
+template <typename Tr, int KB>
+struct BwdStage {
+    struct Regs {
+        uint32_t q[8];
+        float a[8];
+    };
+    struct Pending {
+        float2 c[2][KB / 2];
+    };
+    const uint8_t* wp;
+    const float* wa;
+    const float2* lut;
+    int64_t row_bytes, kblocks;
+    int ng, kg;
+    uint32_t col[KB][4];  // col[c][pair] = rows (2 pair, 2 pair + 1) of column c
+
+    __device__ __forceinline__ void load(int s, Regs& w) const {
+        const int64_t n0 = (int64_t)s * BK;  // N % 64 == 0
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const uint8_t* p = wp + (n0 + r) * row_bytes;
+            if constexpr (KB == 8)
+                w.q[r] = *reinterpret_cast<const uint32_t*>(p);
+            else
+                w.q[r] = *reinterpret_cast<const uint16_t*>(p);
+            w.a[r] = wa[(n0 + r) * kblocks];
+        }
+    }
+    __device__ __forceinline__ void issue(const Regs& w, int pair, Pending& p) const {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < KB / 2; ++b) p.c[h][b] = lut[((w.q[2 * pair + h] >> (8 * b)) & 0xFFu) * LUT_COPIES];
+    }
+    __device__ __forceinline__ void finish(const Regs& w, int pair, const Pending& p, uint4*) {
+        float v[2][KB];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float a = w.a[2 * pair + h];
+#pragma unroll
+            for (int b = 0; b < KB / 2; ++b) {
+                v[h][2 * b] = opaque(p.c[h][b].x * a);
+                v[h][2 * b + 1] = opaque(p.c[h][b].y * a);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < KB; ++c) col[c][pair] = Tr::pack2(v[0][c], v[1][c]);
+    }
+    __device__ __forceinline__ void flush(uint4* dst) const {
+#pragma unroll
+        for (int c = 0; c < KB; ++c) dst[swz(kg * KB + c, ng)] = make_uint4(col[c][0], col[c][1], col[c][2], col[c][3]);
+    }
+    __device__ __forceinline__ void store_all(const Regs& w, uint4* dst) {
+#pragma unroll
+        for (int pair = 0; pair < 4; ++pair) {
+            Pending p;
+            issue(w, pair, p);
+            finish(w, pair, p, dst);
+        }
+        flush(dst);
+    }
+};
+
+template <typename Tr, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
+    constexpr int NW = WM * WN, NT = NW * 64;
+    constexpr int FX = BM / WM / 32;
+    constexpr int FW = BN / WN / 32;
+    constexpr int KB = 8 * BN / NT;  // k columns per thread block: 8 n-groups x (BN / KB) k-groups = NT
+    static_assert(BM % (8 * NW) == 0 && (KB == 4 || KB == 8), "tile / wave mismatch");
+    __shared__ float2 lut_all[256 * LUT_COPIES];
+    __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
+    __shared__ uint4 sB0[BN * 8], sB1[BN * 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wk = wave & 1;
-    lut[tid] = make_float2(kLevelsDev[tid >> 4], kLevelsDev[tid & 15]);
+    const int wm = wave / WN, wn = wave % WN;
+    fill_lut<NT>(lut_all, tid);
 
     const Group grp = group_of(g, blockIdx.y);
     const int64_t K = g.K, N = g.N;
-    const int64_t ntk = (K + BKO - 1) / BKO;
-    const int64_t m0 = (int64_t)(blockIdx.x / ntk) * BM;
-    const int64_t k0 = (int64_t)(blockIdx.x % ntk) * BKO;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN;
+    int64_t tm, tk;
+    tile_coords(blockIdx.x, ntm, ntk, tm, tk);
+    const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) return;
 
     const uint16_t* __restrict__ DY = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N;
     const int64_t kblocks = K / g.blocksize;
     const int bshift = ilog2(g.blocksize);
 
-    const int xa_row = tid >> 3, xa_chunk = tid & 7;
-    // W slice: 8 rows (n-group ng) x 4 columns (k-group kg)
-    const int ng = tid & 7, kg = tid >> 3;
-    const int64_t wk_col = k0 + kg * 4;
-    const bool wk_ok = wk_col < K;
-    const int64_t wk_blk = wk_col >> bshift;
+    BwdStage<Tr, KB> ws;
+    ws.ng = tid & 7;
+    ws.kg = tid >> 3;
+    int64_t kc = k0 + ws.kg * KB;
+    kc = kc < K ? kc : K - KB;  // columns past K only feed outputs that are never stored
+    ws.wp = grp.packed + (int64_t)(ws.ng * 8) * (K / 2) + kc / 2;
+    ws.wa = grp.absmax + (int64_t)(ws.ng * 8) * kblocks + (kc >> bshift);
+    ws.lut = lut_all + (lane & (LUT_COPIES - 1));
+    ws.row_bytes = K / 2;
+    ws.kblocks = kblocks;
 
-    uint4 xr[4];
-    uint32_t wr[8];
-    float ar[8];
-    auto gload = [&](int nt) {
-        const int64_t n0 = (int64_t)nt * BR;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t row = m0 + xa_row + 32 * i;
-            xr[i] = make_uint4(0, 0, 0, 0);
-            if (row < grp.rows) xr[i] = *reinterpret_cast<const uint4*>(DY + row * N + n0 + xa_chunk * 8);
-        }
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int64_t n = n0 + ng * 8 + r;  // N % 64 == 0: always < N
-            wr[r] = 0u;
-            ar[r] = 0.0f;
-            if (wk_ok) {
-                wr[r] = *reinterpret_cast<const uint16_t*>(grp.packed + n * (K / 2) + wk_col / 2);
-                ar[r] = grp.absmax[n * kblocks + wk_blk];
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sA[buf][swz(xa_row + 32 * i, xa_chunk)] = xr[i];
-        // element (row r, column c) of the 8x4 slice: byte c/2 of wr[r], high nibble for even c
-        float v[4][8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const float2 lo = lut[wr[r] & 0xFFu], hi = lut[(wr[r] >> 8) & 0xFFu];
-            v[0][r] = opaque(lo.x * ar[r]);
-            v[1][r] = opaque(lo.y * ar[r]);
-            v[2][r] = opaque(hi.x * ar[r]);
-            v[3][r] = opaque(hi.y * ar[r]);
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            uint4 o;
-            o.x = Tr::pack2(v[c][0], v[c][1]);
-            o.y = Tr::pack2(v[c][2], v[c][3]);
-            o.z = Tr::pack2(v[c][4], v[c][5]);
-            o.w = Tr::pack2(v[c][6], v[c][7]);
-            sB[buf][swz(kg * 4 + c, ng)] = o;
-        }
-    };
+    f32x16_t acc[FW][FX];
+    zero_acc(acc);
+    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, DY, N, m0, grp.rows, (int)(N / BK), sA0, sA1, sB0, sB1, ws, wave,
+                                             lane);
 
-    f32x16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    const int NTILES = (int)(N / BR);
-    gload(0);
-    __syncthreads();
-    lstore(0);
-    __syncthreads();
-
-    for (int nt = 0; nt < NTILES; ++nt) {
-        const int cur = nt & 1;
-        if (nt + 1 < NTILES) gload(nt + 1);
-#pragma unroll
-        for (int kk = 0; kk < BR / 16; ++kk) {
-            uint4 a[2], b[2];
-            const int ch = kk * 2 + (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = sA[cur][swz(wm * 64 + i * 32 + (lane & 31), ch)];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = sB[cur][swz(wk * 64 + j * 32 + (lane & 31), ch)];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma<Tr>(a[i], b[j], acc[i][j]);
-        }
-        if (nt + 1 < NTILES) lstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    const int64_t row_base = m0 + wm * 64, col_base = k0 + wk * 64;
+    const int64_t col_base = k0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
     if (g.lora_rank > 0)
-        lora_term<Tr>(acc, reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base, grp.rows,
-                      reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K, g.lora_rank, lane);
-    store_tile<Tr>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, row_base, grp.rows, col_base, K,
-                   nullptr, lane);
+        lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
+                              reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
+                              grp.rows, g.lora_rank, lane);
+    store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, col_base, K, row_base, grp.rows,
+                           nullptr, lane);
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_fwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
+    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    if (tiles == 0) return STM_OK;
+    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
+    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(WM * WN * 64);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemm_fwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL((k_gemm_fwd<F16, BM, BN, WM, WN>), grid, block, 0, stream, g);
+    return check_launch("gemm_fwd");
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
+    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.K + BN - 1) / BN);
+    if (tiles == 0) return STM_OK;
+    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535)
+        return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
+    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(WM * WN * 64);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemm_bwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL((k_gemm_bwd<F16, BM, BN, WM, WN>), grid, block, 0, stream, g);
+    return check_launch("gemm_bwd_dx");
 }
 
 }  // namespace
 
+// Large problems take the big tile; when it would leave most CUs idle (few
+// activation rows, or small weights) the 128 x 128 tile is used instead.
 int launch_gemm_fwd(const GemmArgs& g, int dtype, hipStream_t stream) {
-    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    if (tiles == 0) return STM_OK;
-    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(NT);
-    if (dtype == STM_BF16)
-        hipLaunchKernelGGL(k_gemm_fwd<BF16>, grid, block, 0, stream, g);
-    else
-        hipLaunchKernelGGL(k_gemm_fwd<F16>, grid, block, 0, stream, g);
-    return check_launch("gemm_fwd");
+    const int64_t big = ((g.M + STM_FWD_BM - 1) / STM_FWD_BM) * ((g.N + STM_FWD_BN - 1) / STM_FWD_BN) * g.num_groups;
+    if (big >= 512) return launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream);
+    return launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
 }
 
 int launch_gemm_bwd(const GemmArgs& g, int dtype, hipStream_t stream) {
-    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.K + 127) / 128);
-    if (tiles == 0) return STM_OK;
-    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535)
-        return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(NT);
-    if (dtype == STM_BF16)
-        hipLaunchKernelGGL(k_gemm_bwd<BF16>, grid, block, 0, stream, g);
-    else
-        hipLaunchKernelGGL(k_gemm_bwd<F16>, grid, block, 0, stream, g);
-    return check_launch("gemm_bwd_dx");
+    const int64_t big = ((g.M + STM_BWD_BM - 1) / STM_BWD_BM) * ((g.K + STM_BWD_BN - 1) / STM_BWD_BN) * g.num_groups;
+    if (big >= 512) return launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream);
+    return launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
 }
 
 }  // namespace stm

@@ -136,8 +136,9 @@ def test_cache_roundtrip_and_from_cache(cuda, tmp_path):
     p1, p2 = getattr(m1.q_proj.weight, NF4_ATTR), getattr(m2.q_proj.weight, NF4_ATTR)
     assert torch.equal(p1.quantized, p2.quantized) and torch.equal(p1.absmax, p2.absmax)
     m3 = _Block()
-    for prm in (m3.q_proj.weight, m3.experts):  # weights never materialised on the host
-        prm.data = torch.empty(prm.shape, dtype=prm.dtype, device="meta")
+    # weights never materialised on the host: meta parameters, as in a meta-device build
+    m3.q_proj.weight = nn.Parameter(torch.empty(512, 256, dtype=torch.float16, device="meta"), requires_grad=False)
+    m3.experts = nn.Parameter(torch.empty(4, 128, 64, dtype=torch.float16, device="meta"), requires_grad=False)
     s3 = prepare_nf4_from_cache(m3, tmp_path, verbose=False)
     assert s3 is not None and s3.tensors == 2 and s3.cache_hits == 2
     assert m3.q_proj.weight.device.type == "cpu" and m3.q_proj.weight.numel() == 0
