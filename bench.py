@@ -195,6 +195,34 @@ def run_lora_step(args):
     return line
 
 
+def run_profile(args):
+    """Kernel-only pass for rocprofv3 (kernel trace / PMC): each kernel of the
+    step launched `--kernel-reps` times on the default workload, plus a plain
+    1 GiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    import torch
+
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit
+
+    dev = torch.device("cuda:0")
+    N, K, M = 14336, 4096, 8192
+    w = seeded(torch, (N, K), 0, 0.02, torch.float16, dev)
+    packed, state = quantize_4bit(w)
+    state.dtype = torch.bfloat16
+    x = seeded(torch, (M, K), 1, 1.0, torch.bfloat16, dev)
+    dy = seeded(torch, (M, N), 4, 1.0, torch.bfloat16, dev)
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    # calibration: an elementwise kernel that reads 1 GiB and writes 1 GiB
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.kernel_reps):
+        nf4_gemm_fwd(x, packed, state.absmax, (N, K), 64)
+        nf4_gemm_bwd_dx(dy, packed, state.absmax, (N, K), 64)
+        dequantize_4bit(packed, state, out=out)
+        torch.mul(src, 2.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "done", "reps": args.kernel_reps, "copy_bytes": 4 * src.numel()}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,6 +232,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="launch each kernel --kernel-reps times for rocprofv3; prints no bench line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -211,6 +241,9 @@ def main():
               "the NF4 path is sharded by weight rows with no collective on one GPU's share -- "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.profile:
+        run_profile(args)
+        return
     line = run_lora_step(args)
     print(json.dumps(line), flush=True)
 

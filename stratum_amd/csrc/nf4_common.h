@@ -47,14 +47,18 @@ __device__ __forceinline__ float opaque(float v) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 struct BF16 {
     typedef bf16x8_t vec8;
     static constexpr int tag = STM_BF16;
+    // two fp32 -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32)
     __device__ static inline uint32_t pack2(float lo, float hi) {
-        __bf16 a = (__bf16)lo, b = (__bf16)hi;  // round to nearest even
-        return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+        const f32x2_t v = {lo, hi};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
     }
     __device__ static inline float to_f32(uint16_t bits) { return __uint_as_float((uint32_t)bits << 16); }
     __device__ static inline uint16_t from_f32(float v) {
@@ -66,9 +70,10 @@ struct BF16 {
 struct F16 {
     typedef f16x8_t vec8;
     static constexpr int tag = STM_F16;
+    // two fp32 -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32)
     __device__ static inline uint32_t pack2(float lo, float hi) {
-        _Float16 a = (_Float16)lo, b = (_Float16)hi;  // round to nearest even
-        return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+        const f32x2_t v = {lo, hi};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
     }
     __device__ static inline float to_f32(uint16_t bits) { return (float)__builtin_bit_cast(_Float16, bits); }
     __device__ static inline uint16_t from_f32(float v) {

@@ -139,23 +139,36 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t nt
     tn = in / gsize;
 }
 
-// Copy the activation tile rows [m0, m0 + BM) x [k0, k0 + 64) into LDS buffer
-// `dst` (BM x 8 chunks). Rows past the valid range re-read the last valid row:
-// they only feed output rows that are never stored.
+// Activation staging: the tile rows [m0, m0 + BM) x [k0, k0 + 64) are copied
+// into an LDS buffer (BM x 8 chunks) with XI direct copies per wave per step.
+// Per-lane global row pointers and the wave-uniform LDS bases of both buffers
+// are computed once; a step only adds k0. Rows past the valid range re-read the
+// last valid row: they only feed output rows that are never stored.
 template <int BM, int NW>
-__device__ __forceinline__ void stage_act(const uint16_t* __restrict__ src, int64_t ld, int64_t m0, int64_t rows,
-                                          int64_t k0, const uint4* dst, int wave, int lane) {
-    constexpr int XI = BM / (8 * NW);
+struct ActStage {
+    static constexpr int XI = BM / (8 * NW);
+    const uint16_t* src[XI];
+    uint32_t lds[2][XI];
+
+    __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int64_t m0, int64_t rows, const uint4* buf0,
+                                         const uint4* buf1, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < XI; ++i) {
-        const int r0 = (wave * XI + i) * 8;
-        const int r = r0 + (lane >> 3);
-        const int c = (lane & 7) ^ swz_key(r);
-        int64_t row = m0 + r;
-        row = row < rows ? row : rows - 1;
-        dma16(src + row * ld + k0 + c * 8, __builtin_amdgcn_readfirstlane(lds_offset(dst + r0 * 8)));
+        for (int i = 0; i < XI; ++i) {
+            const int r0 = (wave * XI + i) * 8;
+            const int r = r0 + (lane >> 3);
+            const int c = (lane & 7) ^ swz_key(r);
+            int64_t row = m0 + r;
+            row = row < rows ? row : rows - 1;
+            src[i] = base + row * ld + c * 8;
+            lds[0][i] = __builtin_amdgcn_readfirstlane(lds_offset(buf0 + r0 * 8));
+            lds[1][i] = __builtin_amdgcn_readfirstlane(lds_offset(buf1 + r0 * 8));
+        }
     }
-}
+    __device__ __forceinline__ void issue(int64_t k0, int buf) const {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) dma16(src[i] + k0, lds[buf][i]);
+    }
+};
 
 // Level table: entry (byte b, copy c) = (level[b >> 4], level[b & 15]) at
 // index 16 b + c. Lane l reads copy l % 16, so the 16 lanes of one LDS pass of
@@ -282,8 +295,10 @@ __device__ __forceinline__ void run_pipeline(f32x16_t (&acc)[FW][FX], const uint
     const int wn = wave % WN, wm = wave / WN;
     const int wrow0 = wn * (BN / WN), xrow0 = wm * (BM / WM);
     typename WS::Regs w0, w1;
+    ActStage<BM, NW> as;
+    as.init(act, ld, m0, rows, sA0, sA1, wave, lane);
 
-    stage_act<BM, NW>(act, ld, m0, rows, 0, sA0, wave, lane);
+    as.issue(0, 0);
     ws.load(0, w0);
     __syncthreads();  // level table ready
     ws.store_all(w0, sB0);
@@ -291,11 +306,11 @@ __device__ __forceinline__ void run_pipeline(f32x16_t (&acc)[FW][FX], const uint
     wait_vmem();
     __syncthreads();
 
-    auto step = [&](int s, const uint4* sAc, const uint4* sBc, uint4* sAn, uint4* sBn, typename WS::Regs& wcur,
+    auto step = [&](int s, const uint4* sAc, const uint4* sBc, int next_buf, uint4* sBn, typename WS::Regs& wcur,
                     typename WS::Regs& wnext) {
         const int s1 = s + 1 < KT ? s + 1 : KT - 1;
         const int s2 = s + 2 < KT ? s + 2 : KT - 1;
-        stage_act<BM, NW>(act, ld, m0, rows, (int64_t)s1 * BK, sAn, wave, lane);
+        as.issue((int64_t)s1 * BK, next_buf);
         ws.load(s2, wnext);
         typename WS::Pending pend[2];
         ws.issue(wcur, 0, pend[0]);
@@ -313,8 +328,8 @@ __device__ __forceinline__ void run_pipeline(f32x16_t (&acc)[FW][FX], const uint
     };
     int s = 0;
     for (; s + 1 < KT; s += 2) {
-        step(s, sA0, sB0, sA1, sB1, w1, w0);
-        step(s + 1, sA1, sB1, sA0, sB0, w0, w1);
+        step(s, sA0, sB0, 1, sB1, w1, w0);
+        step(s + 1, sA1, sB1, 0, sB0, w0, w1);
     }
     if (s < KT) {
 #pragma unroll
