@@ -192,7 +192,189 @@ def run_lora_step(args):
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, w, N, K, args.cpu_rows)
+    if not args.main_only:
+        del x, A, B, dy, out, w
+        torch.cuda.empty_cache()
+        line["configs"] = {
+            "roundtrip_f16_5632x2048": run_roundtrip(torch, args),
+            "qwen3_0.6b_layer_fwd_m4096": run_qwen06(torch, args),
+            "moe_128x_gate_up_down_8192tok_top8": run_moe(torch, args),
+            "stream_8b_layers_pinned_h2d_dequant": run_layer_stream(torch, args),
+        }
     return line
+
+
+# ---------------------------------------------------------------- other configs
+def _gpu_quantized(torch, shape, seed, dev):
+    """fp16 N(0, 0.02) weight generated on the GPU and quantized there."""
+    from stratum_amd.functional import quantize_4bit
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = (torch.randn(*shape, generator=g, device=dev) * 0.02).half()
+    packed, state = quantize_4bit(w.reshape(-1, shape[-1]))
+    del w
+    return packed, state
+
+
+def run_roundtrip(torch, args):
+    """fp16 [5632, 2048] N(0, 0.02): GPU quantize + dequantize vs the C oracle on the host."""
+    import numpy as np
+
+    from stratum_amd.functional import dequantize_4bit, quantize_4bit
+    dev = torch.device("cuda:0")
+    w = seeded(torch, (5632, 2048), 0, 0.02, torch.float16, dev)
+    n = w.numel()
+    packed, state = quantize_4bit(w)
+    out = torch.empty_like(w)
+    q_ms = event_time_ms(torch, lambda: quantize_4bit(w), 50)
+    d_ms = event_time_ms(torch, lambda: dequantize_4bit(packed, state, out=out), 50)
+    byt = 2.5625 * n
+    res = {"shape": [5632, 2048], "quantize_gbs": round(byt / q_ms / 1e6, 1), "quantize_us": round(q_ms * 1e3, 2),
+           "dequantize_gbs": round(byt / d_ms / 1e6, 1), "dequantize_us": round(d_ms * 1e3, 2)}
+    if not args.no_cpu:
+        from oracle import c_oracle as C
+        from oracle import nf4_oracle as O
+        threads = os.cpu_count() or 1
+        bits = w.cpu().view(torch.int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 2.0:
+            p_, a_ = C.quantize(bits, O.DT_F16, 64, "argmin", threads)
+            C.dequantize(p_, a_, n, 64, O.DT_F16, threads)
+            reps += 1
+        cpu_s = (time.perf_counter() - t0) / reps
+        res["cpu_roundtrip_ms"] = round(cpu_s * 1e3, 2)
+        res["cpu_threads"] = threads
+        res["gpu_roundtrip_ms"] = round(q_ms + d_ms, 4)
+    return res
+
+
+def run_qwen06(torch, args):
+    """Qwen3-0.6B layer projections, fused NF4 forward at M = 4096 tokens."""
+    from stratum_amd.functional import nf4_gemm_fwd
+    dev = torch.device("cuda:0")
+    M = 4096
+    shapes = {"q": (2048, 1024), "k": (1024, 1024), "v": (1024, 1024), "o": (1024, 2048),
+              "gate": (3072, 1024), "up": (3072, 1024), "down": (1024, 3072)}
+    ws = {k: _gpu_quantized(torch, s, i, dev) for i, (k, s) in enumerate(shapes.items())}
+    xs = {K: seeded(torch, (M, K), 100 + K, 1.0, torch.bfloat16, dev) for K in {s[1] for s in shapes.values()}}
+
+    def layer():
+        for k, (N, K) in shapes.items():
+            p, st = ws[k]
+            nf4_gemm_fwd(xs[K], p, st.absmax, (N, K), 64)
+
+    ms = event_time_ms(torch, layer, 20)
+    flops = sum(2.0 * M * N * K for N, K in shapes.values())
+    return {"tokens": M, "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
+            "gflop_per_layer": round(flops / 1e9, 2)}
+
+
+def run_layer_stream(torch, args):
+    """8B-class decoder layers (q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096,
+    down 4096x14336) streamed from pinned host payloads: H2D alone, dequantize
+    alone, serial (upload then dequantize per layer, one stream) and overlapped
+    (NF4LayerStream: copy stream + dequant stream)."""
+    import torch.nn as nn
+
+    from stratum_amd.functional import dequantize_4bit
+    from stratum_amd.stream import NF4LayerStream
+    from stratum_amd.upload import NF4_ATTR, NF4Payload, _pin_cpu, ensure_weights, free_weights
+    dev = torch.device("cuda:0")
+    shapes = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+              "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+    layers = []
+    for li in range(args.layers):
+        m = nn.Module()
+        for j, (name, shp) in enumerate(shapes.items()):
+            packed, st = _gpu_quantized(torch, shp, 1000 * li + j, dev)
+            p = nn.Parameter(torch.empty(0, dtype=torch.float16), requires_grad=False)
+            setattr(p, NF4_ATTR, NF4Payload(quantized=_pin_cpu(packed), absmax=_pin_cpu(st.absmax),
+                                            code=_pin_cpu(st.code), shape=shp, dtype=torch.float16, blocksize=64,
+                                            quant_type="nf4", source_numel=shp[0] * shp[1],
+                                            source_bytes=2 * shp[0] * shp[1],
+                                            payload_bytes=packed.numel() + 4 * st.absmax.numel() + 64))
+            m.register_parameter(name, p)
+        layers.append(m)
+    payload = sum(getattr(p, NF4_ATTR).quantized.numel() + 4 * getattr(p, NF4_ATTR).absmax.numel()
+                  for p in layers[0].parameters())
+    elems = sum(a * b for a, b in shapes.values())
+    L = len(layers)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    dev_payloads = [[(getattr(p, NF4_ATTR).quantized.to(dev), getattr(p, NF4_ATTR).absmax.to(dev))
+                     for p in m.parameters()] for m in layers[:2]]
+
+    def h2d_only():
+        for m in layers:
+            for p in m.parameters():
+                pay = getattr(p, NF4_ATTR)
+                pay.quantized.to(dev, non_blocking=True)
+                pay.absmax.to(dev, non_blocking=True)
+
+    outs = {name: torch.empty(shp, dtype=torch.float16, device=dev) for name, shp in shapes.items()}
+
+    def deq_only():
+        for li in range(L):
+            for (q, a), (name, shp) in zip(dev_payloads[li % 2], shapes.items()):
+                dequantize_4bit(q, absmax=a, shape=shp, blocksize=64, dtype=torch.float16, out=outs[name])
+
+    def serial():
+        for m in layers:
+            ensure_weights(m, 0)
+            free_weights(m)
+
+    def overlapped():
+        for _i, _m in NF4LayerStream(layers, 0, lookahead=1):
+            pass
+
+    serial()
+    overlapped()
+    t_h2d = min(timed(h2d_only) for _ in range(2))
+    t_deq = min(timed(deq_only) for _ in range(2))
+    t_ser = min(timed(serial) for _ in range(2))
+    t_ovl = min(timed(overlapped) for _ in range(2))
+    return {"layers": L, "payload_mb_per_layer": round(payload / 1e6, 1),
+            "h2d_gbs": round(payload * L / t_h2d / 1e9, 2),
+            "dequant_gbs": round(2.5625 * elems * L / t_deq / 1e9, 1),
+            "serial_ms": round(t_ser * 1e3, 2), "overlapped_ms": round(t_ovl * 1e3, 2),
+            "h2d_ms": round(t_h2d * 1e3, 2), "dequant_ms": round(t_deq * 1e3, 2),
+            "overlap_efficiency": round(t_ser / t_ovl, 3),
+            "overlapped_vs_h2d_bound": round(t_h2d / t_ovl, 3)}
+
+
+def run_moe(torch, args):
+    """Qwen3-30B-A3B-like expert bank: 128 experts, gate_up [1536, 2048] and
+    down [2048, 768] in NF4; 8192 tokens, top-8 of softmax(N(0,1) logits)."""
+    from stratum_amd.functional import nf4_grouped_gemm
+    dev = torch.device("cuda:0")
+    E, H, I, T, TOPK = 128, 2048, 768, 8192, 8
+    gu_p, gu_s = _gpu_quantized(torch, (E, 2 * I, H), 7, dev)
+    dn_p, dn_s = _gpu_quantized(torch, (E, H, I), 8, dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    logits = torch.randn(T, E, generator=g, device=dev)
+    top = torch.topk(torch.softmax(logits, -1), TOPK, dim=-1).indices.reshape(-1)
+    counts = torch.bincount(top, minlength=E)
+    offsets = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    rows = int(offsets[-1].item())
+    max_rows = int(counts.max().item())
+    x = seeded(torch, (rows, H), 10, 1.0, torch.bfloat16, dev)
+    h = seeded(torch, (rows, I), 11, 1.0, torch.bfloat16, dev)
+
+    def layer():
+        nf4_grouped_gemm(x, gu_p, gu_s.absmax, offsets, (2 * I, H), 64, max_rows=max_rows)
+        nf4_grouped_gemm(h, dn_p, dn_s.absmax, offsets, (H, I), 64, max_rows=max_rows)
+
+    ms = event_time_ms(torch, layer, 20)
+    flops = 2.0 * rows * (2 * I * H + H * I)
+    return {"experts": E, "tokens": T, "top_k": TOPK, "rows": rows, "max_rows_per_expert": max_rows,
+            "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1), "gflop_per_layer": round(flops / 1e9, 1)}
 
 
 def run_profile(args):
@@ -232,6 +414,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--main-only", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--layers", type=int, default=32, help="decoder layers in the stream-in config")
     ap.add_argument("--profile", action="store_true",
                     help="launch each kernel --kernel-reps times for rocprofv3; prints no bench line")
     args = ap.parse_args()

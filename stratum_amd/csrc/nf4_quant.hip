@@ -138,13 +138,14 @@ __global__ __launch_bounds__(64) void k_quantize_generic(const void* __restrict_
 template <int DT>
 static void quantize_vec_dispatch(const void* A, int64_t nfull, int bs, const CellTable& tab, uint8_t* packed,
                                   float* absmax, hipStream_t stream) {
-    // one wave handles 64/L blocks per iteration; size the grid to ~8 iterations per wave
+    // one wave handles 64/L blocks per iteration; one iteration per wave keeps
+    // every load in flight at once (grid-stride beyond 2^20 work-groups)
     const int L = bs >= 512 ? 64 : bs / 8;
     const int64_t per_wave = 64 / L;
     int64_t waves = (nfull + per_wave - 1) / per_wave;
-    int64_t grid = (waves + 4 * 8 - 1) / (4 * 8);
+    int64_t grid = (waves + 3) / 4;
     if (grid < 1) grid = 1;
-    if (grid > 65535) grid = 65535;
+    if (grid > (1 << 20)) grid = 1 << 20;
     uint32_t* p4 = reinterpret_cast<uint32_t*>(packed);
     dim3 g((unsigned)grid), b(256);
     switch (bs) {

@@ -200,3 +200,31 @@ def test_nf4_lora_linear_gradients(cuda):
     assert rel(x.grad, xr.grad) <= 1e-2
     assert rel(lin.lora_A.grad, A.grad) <= 2e-2
     assert rel(lin.lora_B.grad, B.grad) <= 2e-2
+
+
+def test_layer_stream_materialises_each_layer_then_frees_it(cuda):
+    from stratum_amd.stream import NF4LayerStream
+    from stratum_amd.upload import prepare_nf4
+    layers, refs = [], []
+    for i in range(4):
+        l = nn.Linear(256, 384, bias=False, dtype=torch.float16)
+        with torch.no_grad():
+            l.weight.copy_(seeded((384, 256), 40 + i, 0.02, torch.float16))
+        l.weight.requires_grad_(False)
+        refs.append(oracle_dequant_bits(l.weight.detach().clone()))
+        prepare_nf4(l, verbose=False)
+        layers.append(l)
+    x = seeded((32, 256), 50, 1.0, torch.float16).to(cuda)
+    seen = []
+    for i, layer in NF4LayerStream(layers, 0, lookahead=2):
+        np.testing.assert_array_equal(bits16(layer.weight).ravel(), refs[i])
+        y = layer(x)
+        seen.append(i)
+    torch.cuda.synchronize()
+    assert seen == [0, 1, 2, 3]
+    assert all(l.weight.numel() == 0 for l in layers)
+    assert torch.isfinite(y.float()).all()
+    # a second pass re-materialises from the pinned payloads
+    for i, layer in NF4LayerStream(layers, 0, free_after=False):
+        np.testing.assert_array_equal(bits16(layer.weight).ravel(), refs[i])
+    assert all(l.weight.numel() == 384 * 256 for l in layers)
