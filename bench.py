@@ -93,6 +93,18 @@ def cpu_baseline(torch, w_half, N, K, sample_rows):
     }
 
 
+def _profiled_traffic():
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary of this workload (calibrated against a 1 GiB elementwise kernel)."""
+    path = os.path.join(ROOT, "profiles", "traffic_lora_step_w14336x4096_x8192.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return {k: v["read_bytes"] + v["write_bytes"] for k, v in d["kernels"].items()}
+    except (OSError, KeyError, ValueError):
+        return {}
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -162,6 +174,7 @@ def run_lora_step(args):
         return xd @ wt.t()
 
     unf_ms = event_time_ms(torch, unfused, reps)
+    traffic = _profiled_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -179,13 +192,14 @@ def run_lora_step(args):
                    "blocksize": 64, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "kernel": "k_gemm_fwd<BF16>", "achieved": round(fwd_tf, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd"),
                      "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
         "bwd_dx": {"kernel": "k_gemm_bwd<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
         "dequant": {"kernel": "k_dequantize<BF16>", "value": round(deq_gbs, 1), "unit": "GB/s",
                     "frac": round(deq_gbs / HBM_PEAK_GBS, 4), "peak": HBM_PEAK_GBS,
-                    "avg_kernel_ms": round(deq_ms, 4), "bytes_per_launch": deq_bytes},
+                    "avg_kernel_ms": round(deq_ms, 4), "bytes_per_launch": deq_bytes,
+                    "traffic": traffic.get("k_dequantize")},
         "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
                         "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
         "lora_gflop_per_step": round(lora_flops / 1e9, 2),
