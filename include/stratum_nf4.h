@@ -132,6 +132,23 @@ int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const flo
                                 int dtype, void* stream);
 
 /*
+ * SwiGLU gating of a frozen MLP, between the stacked [gate; up] projection and
+ * the down projection. Replaces `act_fn(gate_proj(x)) * up_proj(x)` and its
+ * autograd backward inside MemoryFlatFrozenMLPFunction
+ * (stratum/model/mlp_opt.py:178-180 forward, :203-212 backward recompute),
+ * act_fn = SiLU.
+ *   gate_up:  [rows, 2 * inter], row = [gate_0 .. gate_{inter-1}, up_0 .. up_{inter-1}]
+ *   out:      [rows, inter] = silu(gate) * up
+ *   grad_out: [rows, inter] (gradient of out)
+ *   grad_gate_up: [rows, 2 * inter] = [d gate | d up], the layout of gate_up
+ * fp32 arithmetic, one round-to-nearest-even conversion per output; dtype
+ * STM_BF16 or STM_F16. Asynchronous on `stream`.
+ */
+int stm_swiglu_fwd(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype, void* stream);
+int stm_swiglu_bwd(const void* grad_out, const void* gate_up, void* grad_gate_up, int64_t rows, int64_t inter,
+                   int dtype, void* stream);
+
+/*
  * Host-only introspection used by the CPU test suite (no GPU work):
  * the 15 fp32 decision boundaries of a rounding rule (code > i iff s >= b[i]),
  * and the 65-cell table the quantize kernel indexes with

@@ -40,6 +40,8 @@ SIGNATURES = {
     "stm_nf4_gemm_bwd_dx": ([_P, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _I, _P], _I),
     "stm_nf4_grouped_gemm_fwd": ([_P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
     "stm_nf4_grouped_gemm_bwd_dx": ([_P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
+    "stm_swiglu_fwd": ([_P, _P, _I64, _I64, _I, _P], _I),
+    "stm_swiglu_bwd": ([_P, _P, _P, _I64, _I64, _I, _P], _I),
     "stm_nf4_decision_boundaries": ([_I, _P], _I),
     "stm_nf4_cell_table": ([_I, _P, _P], _I),
 }

@@ -95,6 +95,20 @@ def _aligned(t: torch.Tensor, a: int = 16) -> torch.Tensor:
     return t
 
 
+def _out_buffer(out: Optional[torch.Tensor], shape, dtype, device) -> torch.Tensor:
+    """A fresh output tensor, or ``out`` viewed as ``shape`` after checking it can take the result."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    numel = 1
+    for d in shape:
+        numel *= int(d)
+    if out.dtype != dtype or out.device != device or out.numel() != numel:
+        raise ValueError(f"out must be a {dtype} tensor of {numel} elements on {device}")
+    if not out.is_contiguous() or (numel and out.data_ptr() % 16):
+        raise ValueError("out must be contiguous and 16-byte aligned")
+    return out.view(shape)
+
+
 @torch.no_grad()
 def quantize_4bit(A: torch.Tensor, absmax: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                   blocksize: int = 64, compress_statistics: bool = False, quant_type: str = "nf4",
@@ -197,12 +211,14 @@ def fused_supported(N: int, K: int, blocksize: int, backward: bool = False) -> b
 @torch.no_grad()
 def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, weight_shape: Sequence[int],
                  blocksize: int = 64, bias: Optional[torch.Tensor] = None, lora_t: Optional[torch.Tensor] = None,
-                 lora_b: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 lora_b: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``x @ W.T (+ bias) (+ lora_t @ lora_b.T)`` with W [N, K] in NF4; output dtype = x.dtype.
 
     ``W`` is dequantized inside the kernel with the same rounding as
     ``dequantize_4bit(..., dtype=x.dtype)``. ``lora_t`` [M, R] and ``lora_b`` [N, R]
     (R a multiple of 16) add a rank-R term before the single output rounding.
+    ``out``, if given, is a contiguous, 16-byte aligned tensor of the output's
+    shape and dtype that receives the result.
     """
     N, K = int(weight_shape[0]), int(weight_shape[1])
     if x.shape[-1] != K:
@@ -212,7 +228,7 @@ def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, we
     x2 = _aligned(x.reshape(-1, K))
     M = x2.shape[0]
     dev = x2.device
-    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    y = _out_buffer(out, (M, N), x.dtype, dev)
     b = _aligned(bias.to(x.dtype), 2) if bias is not None else None
     R = 0
     t = lb = None
@@ -235,8 +251,9 @@ def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, we
 @torch.no_grad()
 def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, weight_shape: Sequence[int],
                     blocksize: int = 64, lora_u: Optional[torch.Tensor] = None,
-                    lora_at: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``dy @ W (+ lora_u @ lora_at.T)`` with W [N, K] in NF4; output dtype = dy.dtype."""
+                    lora_at: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``dy @ W (+ lora_u @ lora_at.T)`` with W [N, K] in NF4; output dtype = dy.dtype
+    (``out`` as for :func:`nf4_gemm_fwd`)."""
     N, K = int(weight_shape[0]), int(weight_shape[1])
     if dy.shape[-1] != N:
         raise ValueError(f"dy has {dy.shape[-1]} features, weight has {N} rows")
@@ -245,7 +262,7 @@ def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
     d2 = _aligned(dy.reshape(-1, N))
     M = d2.shape[0]
     dev = d2.device
-    dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
+    dx = _out_buffer(out, (M, K), dy.dtype, dev)
     R = 0
     u = at = None
     if lora_u is not None:
@@ -289,3 +306,49 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
                 int(max_rows), y.data_ptr(), N, K, blocksize, tag, _lib.stream_handle(dev))
     _lib.check(rc, "stm_nf4_grouped_gemm_" + ("bwd_dx" if backward else "fwd"))
     return y
+
+
+@torch.no_grad()
+def swiglu_fwd(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``silu(gate) * up`` of a stacked projection output ``gate_up`` [..., 2 I] = [gate | up].
+
+    fp32 arithmetic and one rounding to ``gate_up.dtype`` (bf16/fp16); the step
+    ``act_fn(gate_proj(x)) * up_proj(x)`` of stratum/model/mlp_opt.py:178-180.
+    """
+    tag = _gemm_dtype(gate_up)
+    two_i = gate_up.shape[-1]
+    if two_i % 2:
+        raise ValueError("gate_up must have an even last dimension [gate | up]")
+    inter = two_i // 2
+    gu = gate_up.reshape(-1, two_i).contiguous()
+    rows = gu.shape[0]
+    dev = gu.device
+    h = _out_buffer(out, (rows, inter), gate_up.dtype, dev) if out is not None else \
+        torch.empty((rows, inter), dtype=gate_up.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_swiglu_fwd(gu.data_ptr(), h.data_ptr(), rows, inter, tag, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_swiglu_fwd")
+    return h.reshape(*gate_up.shape[:-1], inter)
+
+
+@torch.no_grad()
+def swiglu_bwd(grad_out: torch.Tensor, gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Gradient of :func:`swiglu_fwd` with respect to ``gate_up``: [..., 2 I] = [d gate | d up]."""
+    tag = _gemm_dtype(gate_up)
+    two_i = gate_up.shape[-1]
+    inter = two_i // 2
+    if grad_out.shape[-1] != inter or grad_out.dtype != gate_up.dtype:
+        raise ValueError("grad_out must be [..., I] in gate_up's dtype")
+    gu = gate_up.reshape(-1, two_i).contiguous()
+    dh = grad_out.reshape(-1, inter).contiguous()
+    rows = gu.shape[0]
+    if dh.shape[0] != rows:
+        raise ValueError("grad_out and gate_up have different row counts")
+    dev = gu.device
+    dgu = _out_buffer(out, (rows, two_i), gate_up.dtype, dev) if out is not None else \
+        torch.empty((rows, two_i), dtype=gate_up.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_swiglu_bwd(dh.data_ptr(), gu.data_ptr(), dgu.data_ptr(), rows, inter, tag,
+                                       _lib.stream_handle(dev))
+    _lib.check(rc, "stm_swiglu_bwd")
+    return dgu.reshape(*gate_up.shape[:-1], two_i)

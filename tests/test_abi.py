@@ -107,3 +107,24 @@ def test_python_wrapper_raises_value_error_on_bad_arguments():
         F.quantize_4bit(torch.zeros(64, 64), compress_statistics=True)
     with pytest.raises(RuntimeError):
         F.dequantize_4bit(torch.zeros(32, 1, dtype=torch.uint8), absmax=torch.ones(1), shape=(8, 8))
+
+
+def test_swiglu_rejects_bad_arguments(L):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails before any launch
+    assert L.stm_swiglu_fwd(None, fake, 4, 8, 1, None) == -1
+    assert L.stm_swiglu_fwd(fake, fake, 4, 8, 2, None) == -1  # fp32 is not a SwiGLU dtype
+    assert L.stm_swiglu_fwd(fake, fake, -1, 8, 1, None) == -1
+    assert L.stm_swiglu_bwd(fake, None, fake, 4, 8, 0, None) == -1
+    assert L.stm_swiglu_bwd(fake, fake, fake, 4, -8, 0, None) == -1
+    assert b"swiglu" in L.stm_last_error()
+
+
+def test_swiglu_empty_is_a_no_op(L):
+    fake = ctypes.c_void_p(4096)
+    assert L.stm_swiglu_fwd(fake, fake, 0, 8, 1, None) == 0
+    assert L.stm_swiglu_bwd(fake, fake, fake, 16, 0, 0, None) == 0
+
+
+def test_swiglu_empty_accepts_null_pointers(L):
+    assert L.stm_swiglu_fwd(None, None, 0, 8, 1, None) == 0
+    assert L.stm_swiglu_bwd(None, None, None, 5, 0, 0, None) == 0
