@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define STM_NF4_ABI_VERSION 1
+#define STM_NF4_ABI_VERSION 2
 
 /* return codes */
 #define STM_OK 0
@@ -90,11 +90,17 @@ int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, in
  *   dtype        : STM_BF16 or STM_F16, for X, Y, bias, T, L and the dequantized W
  *   X, Y         : row-major, leading dimensions K and N
  *   bias         : NULL or [N];  T, L: NULL (lora_rank = 0) or [M, R], [N, R], R % 16 == 0
+ *   workspace    : NULL, or device memory of at least
+ *                  stm_nf4_gemm_workspace_bytes(M, N, K, 0) bytes (16-byte aligned).
+ *                  When the problem has too few output tiles to fill the GPU
+ *                  (small M) the reduction is split over several work-groups
+ *                  whose fp32 partials go there and are summed (in a fixed
+ *                  order) by a second kernel; NULL disables the split.
  *   constraints  : K % 64 == 0, K % blocksize == 0, all pointers 16-byte aligned
  */
 int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
                      const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K, int blocksize,
-                     int dtype, void* stream);
+                     int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Fused NF4 dequant-GEMM, input gradient of a frozen Linear (no dW: the base
@@ -103,11 +109,21 @@ int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, 
  * Replaces the autograd backward of F.linear on the dequantized weight, run by
  * torch.autograd.backward at stratum/runtime.py:340-341. The optional rank-R term
  * is the LoRA input gradient (U = scale * dY . B, At = A^T).
+ *   workspace    : as stm_nf4_gemm_fwd, sized by stm_nf4_gemm_workspace_bytes(M, N, K, 1)
  *   constraints  : N % 64 == 0, K % 64 == 0, K % blocksize == 0, 16-byte aligned
  */
 int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const void* U, const void* At,
                         int lora_rank, void* dX, int64_t M, int64_t N, int64_t K, int blocksize, int dtype,
-                        void* stream);
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of fp32 workspace the forward (backward = 0) or input-gradient
+ * (backward = 1) GEMM of this size uses to split its reduction: 0 when it does
+ * not split. Host-only, never touches a GPU; negative on invalid sizes.
+ * No counterpart in the reference (bitsandbytes and cuBLAS size their own
+ * scratch); it lets the caller hand in memory from its allocator.
+ */
+int64_t stm_nf4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int backward);
 
 /*
  * Grouped fused NF4 dequant-GEMM over a stacked expert payload, forward:

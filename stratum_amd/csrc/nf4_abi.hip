@@ -174,9 +174,25 @@ static int check_gemm_common(const char* who, const void* a, const uint8_t* pack
     return 1;  // proceed
 }
 
+// Non-NULL workspace: at least the bytes stm_nf4_gemm_workspace_bytes reports.
+static int check_workspace(const char* who, void* workspace, int64_t workspace_bytes, int64_t need) {
+    if (!workspace || need == 0) return STM_OK;
+    if (workspace_bytes < need)
+        return set_error(STM_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", who, (long long)workspace_bytes,
+                         (long long)need);
+    if (!aligned(workspace, 16)) return set_error(STM_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+    return STM_OK;
+}
+
+int64_t stm_nf4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int backward) {
+    g_err[0] = 0;
+    if (M < 0 || N < 0 || K < 0) return set_error(STM_ERR_INVALID, "gemm_workspace_bytes: negative size");
+    return gemm_workspace_bytes(M, N, K, backward != 0, 1);
+}
+
 int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
                      const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K, int blocksize,
-                     int dtype, void* stream) {
+                     int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     int rc = check_gemm_common("gemm_fwd", X, packed, absmax, Y, M, N, K, blocksize, dtype);
     if (rc <= 0) return rc;
@@ -186,16 +202,19 @@ int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, 
     if (lora_rank > 0 && (!T || !L || !aligned(T, 16) || !aligned(L, 16)))
         return set_error(STM_ERR_INVALID, "gemm_fwd: lora_rank > 0 needs 16-byte aligned T and L");
     if (bias && !aligned(bias, 2)) return set_error(STM_ERR_INVALID, "gemm_fwd: misaligned bias");
+    const int64_t need = gemm_workspace_bytes(M, N, K, false, 1);
+    if ((rc = check_workspace("gemm_fwd", workspace, workspace_bytes, need)) != STM_OK) return rc;
     GemmArgs g{};
     g.a = X; g.packed = packed; g.absmax = absmax; g.bias = bias; g.lora_x = lora_rank ? T : nullptr;
     g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
+    g.partial = need ? (float*)workspace : nullptr;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 
 int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const void* U, const void* At,
                         int lora_rank, void* dX, int64_t M, int64_t N, int64_t K, int blocksize, int dtype,
-                        void* stream) {
+                        void* workspace, int64_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     int rc = check_gemm_common("gemm_bwd_dx", dY, packed, absmax, dX, M, N, K, blocksize, dtype);
     if (rc <= 0) return rc;
@@ -206,10 +225,13 @@ int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absm
                          lora_rank);
     if (lora_rank > 0 && (!U || !At || !aligned(U, 16) || !aligned(At, 16)))
         return set_error(STM_ERR_INVALID, "gemm_bwd_dx: lora_rank > 0 needs 16-byte aligned U and At");
+    const int64_t need = gemm_workspace_bytes(M, N, K, true, 1);
+    if ((rc = check_workspace("gemm_bwd_dx", workspace, workspace_bytes, need)) != STM_OK) return rc;
     GemmArgs g{};
     g.a = dY; g.packed = packed; g.absmax = absmax; g.bias = nullptr; g.lora_x = lora_rank ? U : nullptr;
     g.lora_w = lora_rank ? At : nullptr; g.lora_rank = lora_rank; g.out = dX; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
+    g.partial = need ? (float*)workspace : nullptr;
     return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
 }
 

@@ -256,6 +256,41 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FA][FB], uint16
     }
 }
 
+// fp32 partial tile of one split: the same element mapping as store_tile,
+// 16-byte runs (4 consecutive output columns per lane).
+template <int FA, int FB>
+__device__ __forceinline__ void store_tile_f32(const f32x16_t (&acc)[FA][FB], float* __restrict__ out, int64_t ld,
+                                               int64_t ocol_base, int64_t ocols, int64_t orow_base, int64_t orows,
+                                               int lane) {
+#pragma unroll
+    for (int j = 0; j < FB; ++j) {
+        const int64_t orow = orow_base + j * 32 + (lane & 31);
+        if (orow >= orows) continue;
+        float* dst = out + orow * ld;
+#pragma unroll
+        for (int i = 0; i < FA; ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t col = ocol_base + i * 32 + 8 * q + 4 * (lane >> 5);
+                if (col + 3 < ocols) {
+                    *reinterpret_cast<float4*>(dst + col) =
+                        make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < ocols) dst[col + e] = acc[i][j][4 * q + e];
+                }
+            }
+        }
+    }
+}
+
+// Step range of split z of `steps` reduction steps.
+__device__ __forceinline__ void split_range(int steps, int splits, int z, int& begin, int& count) {
+    begin = (int)(((int64_t)z * steps) / splits);
+    count = (int)(((int64_t)(z + 1) * steps) / splits) - begin;
+}
+
 // One 16-deep MFMA sub-step kk of a 64-deep step.
 template <typename Tr, int FA, int FB>
 __device__ __forceinline__ void mma_kk(f32x16_t (&acc)[FA][FB], const uint4* sw, int wrow0, const uint4* sx,
@@ -355,9 +390,10 @@ struct FwdStage {
     const float* wa[WC];
     const float2* lut;
     int tid, bshift;
+    int64_t kbase;  // first reduction index of this work-group's step range
 
     __device__ __forceinline__ void load(int s, Regs& w) const {
-        const int64_t k0 = (int64_t)s * BK;
+        const int64_t k0 = kbase + (int64_t)s * BK;
 #pragma unroll
         for (int j = 0; j < WC; ++j) {
             w.q[j] = *reinterpret_cast<const uint4*>(wp[j] + k0 / 2);
@@ -422,13 +458,16 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) return;
 
-    const uint16_t* __restrict__ X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K;
+    int s_begin, KT;
+    split_range((int)(K / BK), g.splits, blockIdx.z, s_begin, KT);
+    const uint16_t* __restrict__ X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K + (int64_t)s_begin * BK;
     const int64_t kblocks = K / g.blocksize;
 
     FwdStage<Tr, WC, NT> ws;
     ws.lut = lut_all + (lane & (LUT_COPIES - 1));
     ws.tid = tid;
     ws.bshift = ilog2(g.blocksize);
+    ws.kbase = (int64_t)s_begin * BK;
 #pragma unroll
     for (int j = 0; j < WC; ++j) {
         const int cidx = tid + j * NT;
@@ -440,16 +479,19 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
 
     f32x16_t acc[FW][FX];
     zero_acc(acc);
-    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, X, K, m0, grp.rows, (int)(K / BK), sA0, sA1, sB0, sB1, ws, wave,
-                                             lane);
+    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, X, K, m0, grp.rows, KT, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = n0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
-    if (g.lora_rank > 0)
+    if (g.lora_rank > 0 && blockIdx.z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
                               grp.rows, g.lora_rank, lane);
-    store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, col_base, N, row_base, grp.rows,
-                           reinterpret_cast<const uint16_t*>(g.bias), lane);
+    if (g.splits > 1)
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)blockIdx.z * g.M * N, N, col_base, N, row_base, grp.rows,
+                               lane);
+    else
+        store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, col_base, N, row_base,
+                               grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane);
 }
 
 // ----------------------------------------------------------------- backward
@@ -472,11 +514,12 @@ struct BwdStage {
     const float* wa;
     const float2* lut;
     int64_t row_bytes, kblocks;
+    int64_t nbase;  // first reduction index (weight row) of this work-group's step range
     int ng, kg;
     uint32_t col[KB][4];  // col[c][pair] = rows (2 pair, 2 pair + 1) of column c
 
     __device__ __forceinline__ void load(int s, Regs& w) const {
-        const int64_t n0 = (int64_t)s * BK;  // N % 64 == 0
+        const int64_t n0 = nbase + (int64_t)s * BK;  // N % 64 == 0
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const uint8_t* p = wp + (n0 + r) * row_bytes;
@@ -545,11 +588,14 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) return;
 
-    const uint16_t* __restrict__ DY = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N;
+    int s_begin, NT_steps;
+    split_range((int)(N / BK), g.splits, blockIdx.z, s_begin, NT_steps);
+    const uint16_t* __restrict__ DY = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N + (int64_t)s_begin * BK;
     const int64_t kblocks = K / g.blocksize;
     const int bshift = ilog2(g.blocksize);
 
     BwdStage<Tr, KB> ws;
+    ws.nbase = (int64_t)s_begin * BK;
     ws.ng = tid & 7;
     ws.kg = tid >> 3;
     int64_t kc = k0 + ws.kg * KB;
@@ -562,16 +608,64 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
 
     f32x16_t acc[FW][FX];
     zero_acc(acc);
-    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, DY, N, m0, grp.rows, (int)(N / BK), sA0, sA1, sB0, sB1, ws, wave,
-                                             lane);
+    run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, DY, N, m0, grp.rows, NT_steps, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = k0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
-    if (g.lora_rank > 0)
+    if (g.lora_rank > 0 && blockIdx.z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
                               grp.rows, g.lora_rank, lane);
-    store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, col_base, K, row_base, grp.rows,
-                           nullptr, lane);
+    if (g.splits > 1)
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)blockIdx.z * g.M * K, K, col_base, K, row_base, grp.rows,
+                               lane);
+    else
+        store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, col_base, K, row_base,
+                               grp.rows, nullptr, lane);
+}
+
+// Sum of the split partials [splits][rows][cols] (+ bias), one rounding; four
+// columns per lane (cols % 4 == 0).
+template <typename Tr>
+__global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ partial, int splits, int64_t rows,
+                                                      int64_t cols, const uint16_t* __restrict__ bias,
+                                                      uint16_t* __restrict__ out) {
+    const int64_t total = rows * (cols / 4), plane = rows * cols;
+    for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < total; v += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t e = v * 4;
+        float4 acc = *reinterpret_cast<const float4*>(partial + e);
+        for (int z = 1; z < splits; ++z) {
+            const float4 p = *reinterpret_cast<const float4*>(partial + z * plane + e);
+            acc.x += p.x;
+            acc.y += p.y;
+            acc.z += p.z;
+            acc.w += p.w;
+        }
+        if (bias) {
+            const int64_t c = e % cols;
+            acc.x += Tr::to_f32(bias[c]);
+            acc.y += Tr::to_f32(bias[c + 1]);
+            acc.z += Tr::to_f32(bias[c + 2]);
+            acc.w += Tr::to_f32(bias[c + 3]);
+        }
+        uint2 pk;
+        pk.x = Tr::pack2(acc.x, acc.y);
+        pk.y = Tr::pack2(acc.z, acc.w);
+        *reinterpret_cast<uint2*>(out + e) = pk;
+    }
+}
+
+int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int dtype, hipStream_t stream) {
+    const int64_t items = g.M * (cols / 4);
+    if (items == 0) return STM_OK;
+    const int64_t blocks = (items + 255) / 256;
+    const unsigned grid = (unsigned)(blocks < 16384 ? blocks : 16384);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL(k_split_reduce<BF16>, dim3(grid), dim3(256), 0, stream, g.partial, g.splits, g.M, cols,
+                           (const uint16_t*)bias, (uint16_t*)g.out);
+    else
+        hipLaunchKernelGGL(k_split_reduce<F16>, dim3(grid), dim3(256), 0, stream, g.partial, g.splits, g.M, cols,
+                           (const uint16_t*)bias, (uint16_t*)g.out);
+    return check_launch("gemm split reduce");
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -579,7 +673,7 @@ int launch_fwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (tiles == 0) return STM_OK;
     if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(WM * WN * 64);
+    dim3 grid((unsigned)tiles, (unsigned)g.num_groups, (unsigned)g.splits), block(WM * WN * 64);
     if (dtype == STM_BF16)
         hipLaunchKernelGGL((k_gemm_fwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
     else
@@ -593,7 +687,7 @@ int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
     if (tiles == 0) return STM_OK;
     if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535)
         return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups), block(WM * WN * 64);
+    dim3 grid((unsigned)tiles, (unsigned)g.num_groups, (unsigned)g.splits), block(WM * WN * 64);
     if (dtype == STM_BF16)
         hipLaunchKernelGGL((k_gemm_bwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
     else
@@ -603,18 +697,92 @@ int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
 
 }  // namespace
 
-// Large problems take the big tile; when it would leave most CUs idle (few
-// activation rows, or small weights) the 128 x 128 tile is used instead.
-int launch_gemm_fwd(const GemmArgs& g, int dtype, hipStream_t stream) {
-    const int64_t big = ((g.M + STM_FWD_BM - 1) / STM_FWD_BM) * ((g.N + STM_FWD_BN - 1) / STM_FWD_BN) * g.num_groups;
-    if (big >= 512) return launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream);
-    return launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+namespace {
+
+// Tile shape and split count of a problem: `cols` = output columns (N forward,
+// K input gradient), `red` = reduction length (K forward, N input gradient).
+// Both tile shapes run one work-group per CU (LDS), so a launch runs in waves
+// of 256 work-groups (MI355X's CU count). Estimated time of a choice:
+//   waves(tiles * splits) * (steps_per_split * t_step + t_wave) + reduce,
+// t_step = time of one 64-deep step of one wave of tiles, measured at
+// M = 2048..8192 on the 14336 x 4096 and 4096 x 14336 weights (forward: 2.0 us
+// big tile, 0.8 us 128 x 128; input gradient: 2.4 us, 1.35 us), t_wave = 8 us
+// of per-tile prologue and epilogue, reduce = the fp32 partials written and
+// read once at 5 TB/s plus 4 us. Splits: at most 16, at least 8 steps each;
+// grouped launches never split.
+constexpr int kCUs = 256;
+
+struct Plan {
+    bool big;
+    int64_t tiles;
+    int splits;
+};
+
+double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M, int64_t cols) {
+    const int64_t waves = (tiles * sp + kCUs - 1) / kCUs;
+    const int64_t per = (steps + sp - 1) / sp;
+    double t = (double)waves * ((double)per * t_step + 8.0);
+    if (sp > 1) t += ((double)sp * M * cols * 8.0 + (double)M * cols * 2.0) / 5.0e6 + 4.0;  // us
+    return t;
 }
 
-int launch_gemm_bwd(const GemmArgs& g, int dtype, hipStream_t stream) {
-    const int64_t big = ((g.M + STM_BWD_BM - 1) / STM_BWD_BM) * ((g.K + STM_BWD_BN - 1) / STM_BWD_BN) * g.num_groups;
-    if (big >= 512) return launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream);
-    return launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
+    const int64_t bm = backward ? STM_BWD_BM : STM_FWD_BM, bn = backward ? STM_BWD_BN : STM_FWD_BN;
+    const int64_t big_tiles = ((M + bm - 1) / bm) * ((cols + bn - 1) / bn) * num_groups;
+    const int64_t small_tiles = ((M + 127) / 128) * ((cols + 127) / 128) * num_groups;
+    const int64_t steps = red / BK;
+    const double t_big = backward ? 2.4 : 2.0, t_small = backward ? 1.35 : 0.8;
+    int max_sp = 1;
+    if (num_groups == 1) {
+        const int64_t by_steps = steps / 8;
+        max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
+    }
+    Plan best{true, big_tiles, 1};
+    double best_t = plan_cost(big_tiles, steps, 1, t_big, M, cols);
+    for (int sp = 1; sp <= max_sp; ++sp) {
+        const double tb = plan_cost(big_tiles, steps, sp, t_big, M, cols);
+        if (tb < best_t) {
+            best_t = tb;
+            best = Plan{true, big_tiles, sp};
+        }
+        const double ts = plan_cost(small_tiles, steps, sp, t_small, M, cols);
+        if (ts < best_t) {
+            best_t = ts;
+            best = Plan{false, small_tiles, sp};
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
+    return backward ? plan(M, K, N, true, num_groups).splits : plan(M, N, K, false, num_groups).splits;
+}
+
+int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
+    const int sp = gemm_splits(M, N, K, backward, num_groups);
+    return sp > 1 ? (int64_t)sp * M * (backward ? K : N) * (int64_t)sizeof(float) : 0;
+}
+
+int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
+    GemmArgs g = g0;
+    const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
+    g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
+    const int rc = p.big ? launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream)
+                         : launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+    if (rc != STM_OK || g.splits == 1) return rc;
+    return launch_split_reduce(g, g.N, g.bias, dtype, stream);
+}
+
+int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
+    GemmArgs g = g0;
+    const Plan p = plan(g.M, g.K, g.N, true, g.num_groups);
+    g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
+    const int rc = p.big ? launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream)
+                         : launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+    if (rc != STM_OK || g.splits == 1) return rc;
+    return launch_split_reduce(g, g.K, nullptr, dtype, stream);
 }
 
 }  // namespace stm

@@ -24,7 +24,19 @@ struct GemmArgs {
     int blocksize;
     const int32_t* offsets;
     int num_groups;
+    // Split reduction: when splits > 1, work-group z of a tile covers reduction
+    // steps [z * steps / splits, (z + 1) * steps / splits) and stores its fp32 tile
+    // to partial[z][row][col]; a second kernel sums the splits (fixed order),
+    // adds the bias and rounds once.
+    float* partial;
+    int splits;
 };
+
+// Split count the launchers use for a problem (1 = no split) and the fp32
+// workspace it needs: sized so that small-M problems still put >= 512
+// work-groups (two per CU of MI355X's 256) on the GPU.
+int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups);
+int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups);
 
 int launch_quantize(const void* A, int dtype, int64_t n, int blocksize, const CellTable& tab, uint8_t* packed,
                     float* absmax, hipStream_t stream);

@@ -95,6 +95,17 @@ def _aligned(t: torch.Tensor, a: int = 16) -> torch.Tensor:
     return t
 
 
+def _gemm_workspace(M: int, N: int, K: int, backward: bool, device) -> Optional[torch.Tensor]:
+    """fp32 split-reduction workspace for a fused GEMM of this size, from torch's
+    caching allocator (None when the library does not split this problem)."""
+    nbytes = int(_lib.lib().stm_nf4_gemm_workspace_bytes(M, N, K, int(backward)))
+    if nbytes < 0:
+        _lib.check(nbytes, "stm_nf4_gemm_workspace_bytes")
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+
+
 def _out_buffer(out: Optional[torch.Tensor], shape, dtype, device) -> torch.Tensor:
     """A fresh output tensor, or ``out`` viewed as ``shape`` after checking it can take the result."""
     if out is None:
@@ -239,11 +250,13 @@ def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, we
         if lb.shape != (N, R):
             raise ValueError(f"lora_b shape {tuple(lb.shape)} != ({N}, {R})")
     with torch.cuda.device(dev):
+        ws = _gemm_workspace(M, N, K, False, dev)
         rc = _lib.lib().stm_nf4_gemm_fwd(
             x2.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(),
             b.data_ptr() if b is not None else None,
             t.data_ptr() if t is not None else None, lb.data_ptr() if lb is not None else None, R,
-            y.data_ptr(), M, N, K, blocksize, tag, _lib.stream_handle(dev))
+            y.data_ptr(), M, N, K, blocksize, tag, ws.data_ptr() if ws is not None else None,
+            4 * ws.numel() if ws is not None else 0, _lib.stream_handle(dev))
     _lib.check(rc, "stm_nf4_gemm_fwd")
     return y.reshape(*lead, N)
 
@@ -272,10 +285,12 @@ def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
         if at.shape != (K, R):
             raise ValueError(f"lora_at shape {tuple(at.shape)} != ({K}, {R})")
     with torch.cuda.device(dev):
+        ws = _gemm_workspace(M, N, K, True, dev)
         rc = _lib.lib().stm_nf4_gemm_bwd_dx(
             d2.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(),
             u.data_ptr() if u is not None else None, at.data_ptr() if at is not None else None, R,
-            dx.data_ptr(), M, N, K, blocksize, tag, _lib.stream_handle(dev))
+            dx.data_ptr(), M, N, K, blocksize, tag, ws.data_ptr() if ws is not None else None,
+            4 * ws.numel() if ws is not None else 0, _lib.stream_handle(dev))
     _lib.check(rc, "stm_nf4_gemm_bwd_dx")
     return dx.reshape(*lead, K)
 

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version(L):
-    assert L.stm_nf4_abi_version() == 1
+    assert L.stm_nf4_abi_version() == 2
 
 
 @pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
@@ -81,16 +81,16 @@ def test_invalid_arguments_are_rejected_without_a_gpu(L):
     assert L.stm_nf4_dequantize(p, p, 16, 64, p, 7, None) == -1
     assert L.stm_nf4_dequantize(None, None, 0, 64, None, 0, None) == 0
     # K not a multiple of 64 -> unsupported
-    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 100, 64, 1, None) == -2
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 100, 64, 1, None, 0, None) == -2
     assert "multiple of 64" in _err(L)
     # fp32 GEMM is not a thing
-    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 64, 64, 2, None) == -1
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 4, 8, 64, 64, 2, None, 0, None) == -1
     # bad LoRA rank
-    assert L.stm_nf4_gemm_fwd(p, p, p, None, p, p, 8, p, 4, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, p, p, 8, p, 4, 8, 64, 64, 1, None, 0, None) == -1
     # backward needs N % 64 == 0
-    assert L.stm_nf4_gemm_bwd_dx(p, p, p, None, None, 0, p, 4, 40, 64, 64, 1, None) == -2
+    assert L.stm_nf4_gemm_bwd_dx(p, p, p, None, None, 0, p, 4, 40, 64, 64, 1, None, 0, None) == -2
     # misaligned pointer
-    assert L.stm_nf4_gemm_fwd(p + 2, p, p, None, None, None, 0, p, 4, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_gemm_fwd(p + 2, p, p, None, None, None, 0, p, 4, 8, 64, 64, 1, None, 0, None) == -1
     assert L.stm_nf4_grouped_gemm_fwd(p, p, p, None, 4, 16, p, 8, 64, 64, 1, None) == -1
     assert L.stm_nf4_grouped_gemm_fwd(p, p, p, p, 0, 16, p, 8, 64, 64, 1, None) == -1
     assert L.stm_nf4_decision_boundaries(3, p) == -1
@@ -128,3 +128,28 @@ def test_swiglu_empty_is_a_no_op(L):
 def test_swiglu_empty_accepts_null_pointers(L):
     assert L.stm_swiglu_fwd(None, None, 0, 8, 1, None) == 0
     assert L.stm_swiglu_bwd(None, None, None, 5, 0, 0, None) == 0
+
+
+
+def test_gemm_workspace_sizing(L):
+    # large problems fill the GPU with output tiles: no split, no workspace
+    assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 0) == 0
+    assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 1) == 0
+    # M = 16, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
+    # the input gradient's 16 big tiles (4096 output columns) split 16 ways
+    # over the 224 steps of its 14336-long reduction
+    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 2 * 16 * 14336 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 8 * 1 * 4096 * 4
+    # a short reduction caps the split at 8 steps per split
+    assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(16, 256, 256, 0) == 0
+    assert L.stm_nf4_gemm_workspace_bytes(0, 256, 4096, 0) == 0
+    assert L.stm_nf4_gemm_workspace_bytes(-1, 256, 256, 0) < 0
+
+
+def test_gemm_rejects_small_workspace(L):
+    p = ctypes.c_void_p(4096)
+    need = L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0)
+    assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 16, 14336, 4096, 64, 1, p, need - 4, None) == -1
+    assert b"workspace" in L.stm_last_error()

@@ -225,6 +225,52 @@ def test_gemm_bwd_dx_matches_fp32_reference(cuda, dtype, M, N, K, rank):
     assert _rel(dx, ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,backward", [
+    (16, 14336, 4096, False), (1, 4096, 14336, False), (7, 2048, 1024, False),
+    (16, 14336, 4096, True), (3, 4096, 14336, True), (64, 3072, 1024, True),
+])
+def test_split_reduction_matches_fp32_and_unsplit(cuda, dtype, M, N, K, backward):
+    """Small M splits the reduction over work-groups (fp32 partials in a
+    workspace, summed by a second kernel): same result as the reference within
+    tolerance, bias added once, LoRA term once, and within rounding of the
+    unsplit kernel (called through the ABI with no workspace)."""
+    from stratum_amd import _lib
+    from stratum_amd.functional import _gemm_dtype, nf4_gemm_bwd_dx, nf4_gemm_fwd
+    L = _lib.lib()
+    assert L.stm_nf4_gemm_workspace_bytes(M, N, K, int(backward)) > 0, "case must exercise the split path"
+    rp, ra = _nf4_weight(N, K, M + N + K + int(backward))
+    wq = oracle_deq_tensor(rp, ra, (N, K), 64, dtype).to(cuda)
+    packed, absmax = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    R = 16
+    if not backward:
+        x = seeded((M, K), 11, 1.0, dtype).to(cuda)
+        b = seeded((N,), 12, 0.1, dtype).to(cuda)
+        t = seeded((M, R), 13, 0.5, dtype).to(cuda)
+        lb = seeded((N, R), 14, 0.01, dtype).to(cuda)
+        y = nf4_gemm_fwd(x, packed, absmax, (N, K), 64, bias=b, lora_t=t, lora_b=lb)
+        ref = x.float() @ wq.float().t().contiguous() + b.float() + t.float() @ lb.float().t().contiguous()
+        plain = torch.empty_like(y)
+        rc = L.stm_nf4_gemm_fwd(x.data_ptr(), packed.data_ptr(), absmax.data_ptr(), b.data_ptr(), t.data_ptr(),
+                                lb.data_ptr(), R, plain.data_ptr(), M, N, K, 64, _gemm_dtype(x), None, 0,
+                                _lib.stream_handle(x.device))
+    else:
+        dy = seeded((M, N), 15, 1.0, dtype).to(cuda)
+        u = seeded((M, R), 16, 0.5, dtype).to(cuda)
+        at = seeded((K, R), 17, 0.01, dtype).to(cuda)
+        y = nf4_gemm_bwd_dx(dy, packed, absmax, (N, K), 64, lora_u=u, lora_at=at)
+        ref = dy.float() @ wq.float() + u.float() @ at.float().t().contiguous()
+        plain = torch.empty_like(y)
+        rc = L.stm_nf4_gemm_bwd_dx(dy.data_ptr(), packed.data_ptr(), absmax.data_ptr(), u.data_ptr(), at.data_ptr(),
+                                   R, plain.data_ptr(), M, N, K, 64, _gemm_dtype(dy), None, 0,
+                                   _lib.stream_handle(dy.device))
+    assert rc == 0, L.stm_last_error()
+    assert _rel(y, ref) <= TOL[dtype]
+    assert _rel(plain, ref) <= TOL[dtype]
+    # only the fp32 summation order differs: a few elements one 16-bit step apart
+    assert _rel(y, plain.float()) <= TOL[dtype] / 4
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16])
 def test_gemm_full_lora_step_shape(cuda, dtype):
     """W [14336, 4096], X [8192, 4096]: forward and input gradient at full size."""
