@@ -141,14 +141,30 @@ def run_lora_step(args):
         A.grad = None
         B.grad = None
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    def timed_steps(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    # The headline measures the fused dequant-GEMMs (forced for every row count);
+    # the library default for this M (dequantize + hipBLASLt) is reported beside it.
+    policy = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
+    os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = "-1"
+    try:
+        for _ in range(args.warmup):
+            step()
+        elapsed = timed_steps(args.steps)
+    finally:
+        if policy is None:
+            del os.environ["STRATUM_NF4_FUSED_MAX_ROWS"]
+        else:
+            os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = policy
+    step()
+    default_elapsed = timed_steps(max(3, args.steps // 3))
+    default_ms = default_elapsed * 1e3 / max(3, args.steps // 3)
     ms = elapsed * 1e3 / args.steps
     base_flops = 2 * 2.0 * M * N * K
     lora_flops = 2.0 * M * K * R + 2.0 * M * R * N           # forward rank-16 path
@@ -202,6 +218,10 @@ def run_lora_step(args):
                     "traffic": traffic.get("k_dequantize")},
         "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
                         "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
+        "default_policy_step": {"what": "NF4LoRALinear default above 512 rows: dequantize + hipBLASLt, "
+                                        "backward re-dequantizes",
+                                "ms_per_step": round(default_ms, 4),
+                                "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},
         "lora_gflop_per_step": round(lora_flops / 1e9, 2),
     }
     if not args.no_cpu:
@@ -214,6 +234,8 @@ def run_lora_step(args):
             "qwen3_0.6b_layer_fwd_m4096": run_qwen06(torch, args),
             "moe_128x_gate_up_down_8192tok_top8": run_moe(torch, args),
             "stream_8b_layers_pinned_h2d_dequant": run_layer_stream(torch, args),
+            "mlp_8b_swiglu_8192tok_chunk2048_fwd_bwd": run_mlp(torch, args),
+            "small_m16_w14336x4096_split_reduction": run_small_m(torch, args),
         }
     return line
 
@@ -389,6 +411,87 @@ def run_moe(torch, args):
     flops = 2.0 * rows * (2 * I * H + H * I)
     return {"experts": E, "tokens": T, "top_k": TOPK, "rows": rows, "max_rows_per_expert": max_rows,
             "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1), "gflop_per_layer": round(flops / 1e9, 1)}
+
+
+def run_mlp(torch, args):
+    """Frozen 8B SwiGLU MLP (H 4096, I 14336), 8192 tokens in chunks of 2048:
+    forward + input gradient through MemoryFlatFrozenMLP with NF4 projections
+    (library default, and fused kernels forced), against the reference's
+    architecture: the same wrapper over a dense module holding the dequantized
+    bf16 weights (chunked forward and torch.autograd.grad recompute)."""
+    import torch.nn as nn
+    from stratum_amd.functional import dequantize_4bit
+    from stratum_amd.mlp import MemoryFlatFrozenMLP, quantize_mlp_
+    dev = torch.device("cuda:0")
+    H, I, T, CH = 4096, 14336, 8192, 2048
+
+    class Mlp(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = nn.Linear(H, I, bias=False, device=dev, dtype=torch.bfloat16)
+            self.up_proj = nn.Linear(H, I, bias=False, device=dev, dtype=torch.bfloat16)
+            self.down_proj = nn.Linear(I, H, bias=False, device=dev, dtype=torch.bfloat16)
+            self.act_fn = nn.SiLU()
+            for i, lin in enumerate((self.gate_proj, self.up_proj, self.down_proj)):
+                lin.weight.requires_grad_(False)
+                lin.weight.copy_(seeded(torch, tuple(lin.weight.shape), 30 + i, 0.02, torch.float16, dev))
+
+    with torch.no_grad():
+        dense = Mlp()
+    nf4 = quantize_mlp_(Mlp())
+    with torch.no_grad():  # the reference runs on the dequantized weights
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            lin = getattr(nf4, name)
+            getattr(dense, name).weight.copy_(dequantize_4bit(lin.quantized, lin.quant_state, dtype=torch.bfloat16))
+    x = seeded(torch, (1, T, H), 33, 1.0, torch.bfloat16, dev)
+    dy = seeded(torch, (1, T, H), 34, 1.0, torch.bfloat16, dev)
+
+    def run(module):
+        w = MemoryFlatFrozenMLP(module, token_chunk_size=CH)
+
+        def go():
+            xi = x.detach().requires_grad_(True)
+            w(xi).backward(dy)
+        return go
+
+    out = {}
+    flops = 2.0 * T * H * I * 3 * 2  # forward (3 projections) + input gradient (3)
+    for name, fn in (("reference_arch_dense", run(dense)), ("nf4_default", run(nf4))):
+        ms = event_time_ms(torch, fn, 5)
+        out[name] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1)}
+    policy = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
+    os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = "-1"
+    try:
+        ms = event_time_ms(torch, run(nf4), 5)
+    finally:
+        if policy is None:
+            del os.environ["STRATUM_NF4_FUSED_MAX_ROWS"]
+        else:
+            os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = policy
+    out["nf4_fused_forced"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1)}
+    out["model_gflop"] = round(flops / 1e9, 1)
+    out["tokens"], out["chunk"] = T, CH
+    return out
+
+
+def run_small_m(torch, args):
+    """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward and
+    input gradient, whose few output tiles get a split reduction, against
+    dequantize + hipBLASLt."""
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd
+    dev = torch.device("cuda:0")
+    N, K, M = 14336, 4096, 16
+    p, st = _gpu_quantized(torch, (N, K), 40, dev)
+    st.dtype = torch.bfloat16
+    x = seeded(torch, (M, K), 41, 1.0, torch.bfloat16, dev)
+    dy = seeded(torch, (M, N), 42, 1.0, torch.bfloat16, dev)
+    f = event_time_ms(torch, lambda: nf4_gemm_fwd(x, p, st.absmax, (N, K), 64), 50)
+    b = event_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy, p, st.absmax, (N, K), 64), 50)
+    uf = event_time_ms(torch, lambda: x @ dequantize_4bit(p, st).t(), 50)
+    ub = event_time_ms(torch, lambda: dy @ dequantize_4bit(p, st), 50)
+    wbytes = N * K / 2 + 4 * N * K / 64
+    return {"M": M, "fused_fwd_ms": round(f, 4), "fused_bwd_ms": round(b, 4), "unfused_fwd_ms": round(uf, 4),
+            "unfused_bwd_ms": round(ub, 4), "fused_fwd_weight_gbs": round(wbytes / f / 1e6, 1)}
 
 
 def run_profile(args):

@@ -21,7 +21,9 @@ library instead of autograd:
 * the backward of a chunk is ``gu = X Wguᵀ`` (recompute), ``dh = dY Wd``,
   ``dgu = swiglu_bwd(dh, gu)``, ``dX = dgu Wgu``: five GEMM units of
   ``2·rows·H·I`` flops against the reference's six (it also recomputes the
-  down projection's output, which the input gradient does not need).
+  down projection's output, which the input gradient does not need);
+* chunks larger than ``fused_max_rows()`` rows dequantize the stacked weights
+  once per call and run those GEMMs on the library (see ``nf4_linear``).
 
 Chunks are taken over the flattened tokens, ``token_chunk_size`` tokens of
 every batch row at a time, so the peak intermediate is the reference's
@@ -36,8 +38,9 @@ from typing import Any, NamedTuple, Optional
 import torch
 import torch.nn as nn
 
-from .functional import fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit, swiglu_bwd, swiglu_fwd
-from .nf4_linear import NF4Linear
+from .functional import (dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit, swiglu_bwd,
+                         swiglu_fwd)
+from .nf4_linear import NF4Linear, fused_max_rows
 
 __all__ = [
     "MemoryFlatFrozenMLP",
@@ -110,9 +113,32 @@ class NF4StackedMLP:
         return (fused_supported(2 * inter, hidden, blocksize, backward=True)
                 and fused_supported(hidden, inter, blocksize, backward=True))
 
-    def forward_rows(self, x: torch.Tensor, out: torch.Tensor, rows_per_chunk: int) -> None:
-        """``out[r] = down(silu(gate(x[r])) * up(x[r]))`` for the rows of ``x`` [rows, H]."""
+    def _fused(self, rows_per_chunk: int) -> bool:
+        limit = fused_max_rows()
+        return limit < 0 or rows_per_chunk <= limit
+
+    def _dense(self, dtype: torch.dtype):
+        """Dequantized [2 I, H] and [H, I] temporaries for the library-GEMM path."""
         H, I, bs = self.hidden, self.inter, self.blocksize
+        w_gu = dequantize_4bit(self.gu_packed, absmax=self.gu_absmax, blocksize=bs, dtype=dtype, shape=(2 * I, H))
+        w_d = dequantize_4bit(self.d_packed, absmax=self.d_absmax, blocksize=bs, dtype=dtype, shape=(H, I))
+        return w_gu, w_d
+
+    def forward_rows(self, x: torch.Tensor, out: torch.Tensor, rows_per_chunk: int) -> None:
+        """``out[r] = down(silu(gate(x[r])) * up(x[r]))`` for the rows of ``x`` [rows, H].
+
+        Chunks of at most ``fused_max_rows()`` rows run the fused kernels; larger
+        chunks dequantize the stacked weights once for the whole call and run
+        the library GEMM (the faster choice there, see ``nf4_linear``).
+        """
+        H, I, bs = self.hidden, self.inter, self.blocksize
+        if not self._fused(rows_per_chunk):
+            w_gu, w_d = self._dense(x.dtype)
+            for s in range(0, x.shape[0], rows_per_chunk):
+                e = min(s + rows_per_chunk, x.shape[0])
+                h = swiglu_fwd(x[s:e] @ w_gu.t())
+                torch.matmul(h, w_d.t(), out=out[s:e])
+            return
         for s in range(0, x.shape[0], rows_per_chunk):
             e = min(s + rows_per_chunk, x.shape[0])
             gu = nf4_gemm_fwd(x[s:e], self.gu_packed, self.gu_absmax, (2 * I, H), bs)
@@ -122,6 +148,14 @@ class NF4StackedMLP:
     def input_grad_rows(self, x: torch.Tensor, dy: torch.Tensor, dx: torch.Tensor, rows_per_chunk: int) -> None:
         """``dx[r]`` = gradient of the MLP output row r (given ``dy[r]``) with respect to ``x[r]``."""
         H, I, bs = self.hidden, self.inter, self.blocksize
+        if not self._fused(rows_per_chunk):
+            w_gu, w_d = self._dense(x.dtype)
+            for s in range(0, x.shape[0], rows_per_chunk):
+                e = min(s + rows_per_chunk, x.shape[0])
+                gu = x[s:e] @ w_gu.t()
+                dgu = swiglu_bwd(dy[s:e] @ w_d, gu)
+                torch.matmul(dgu, w_gu, out=dx[s:e])
+            return
         for s in range(0, x.shape[0], rows_per_chunk):
             e = min(s + rows_per_chunk, x.shape[0])
             gu = nf4_gemm_fwd(x[s:e], self.gu_packed, self.gu_absmax, (2 * I, H), bs)

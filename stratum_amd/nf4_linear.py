@@ -1,16 +1,28 @@
 """NF4Linear: frozen Linear whose weight stays NF4-packed on the GPU.
 
 Mirrors ``stratum/nf4_linear.py:17-47`` (same constructor, ``in_features`` /
-``out_features`` from ``quant_state.shape``). Where the reference dequantizes the
+``out_features`` from ``quant_state.shape``). The reference dequantizes the
 whole weight to a temporary fp16 tensor and calls ``F.linear``
-(``stratum/nf4_linear.py:46-47``), forward here is one fused dequant-GEMM and
-backward is one fused dequant-GEMM for ``dX = dY . W`` -- the dequantized weight
-never exists in HBM. ``NF4LoRALinear`` adds the PEFT-style LoRA update
-(``scripts/train.py:568-573``: r=16, alpha=16) with its rank-16 term folded into
-the same two kernels.
+(``stratum/nf4_linear.py:46-47``). Here each call picks the faster of two GPU
+paths for its row count M (tokens), measured on MI355X:
 
+* M <= ``fused_max_rows()`` (default 512): one fused dequant-GEMM forward and
+  one fused dequant-GEMM for ``dX = dY . W``; the dequantized weight never
+  exists in HBM, and the packed weight (0.56 B/element) is all the weight
+  traffic -- the fused kernels win or tie there;
+* larger M: ``dequantize_4bit`` into a temporary, then the library GEMM
+  (hipBLASLt), which is 1.3-1.5x faster than the fused kernel from M ~ 2048
+  on, because the dequantization is paid once for all rows instead of once per
+  256-row tile. The backward dequantizes again instead of keeping the
+  temporary alive (23 us for a 14336 x 4096 weight), as the reference's
+  forward/recompute does.
+
+``NF4LoRALinear`` adds the PEFT-style LoRA update (``scripts/train.py:568-573``:
+r=16, alpha=16), folded into the fused kernels' epilogues on the first path.
 Shapes the fused kernels do not take (K not a multiple of 64, ...) and dtypes
-other than bf16/fp16 run ``dequantize_4bit`` + ``F.linear`` on the GPU instead.
+other than bf16/fp16 always take the second path. ``STRATUM_NF4_FUSED_MAX_ROWS``
+overrides the threshold (``-1``: always fused where the shape allows, ``0``:
+never).
 """
 
 from __future__ import annotations
@@ -22,20 +34,37 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+import os
+
 from .functional import (QuantState, dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd)
+
+_DEFAULT_FUSED_MAX_ROWS = 512
+
+
+def fused_max_rows() -> int:
+    """Largest row count (tokens) sent to the fused kernels; -1 = no limit."""
+    v = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
+    return int(v) if v not in (None, "") else _DEFAULT_FUSED_MAX_ROWS
 
 
 class _NF4LinearFn(torch.autograd.Function):
     """y = x . W^T (+ bias) (+ scaling * (x . A^T) . B^T) with W frozen in NF4."""
 
     @staticmethod
-    def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling):
+    def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused):
         t = None
         if lora_a is not None:
             t = (x.reshape(-1, x.shape[-1]) @ lora_a.t().to(x.dtype)) * scaling
-        y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
-                         lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
-        ctx.shape, ctx.blocksize, ctx.scaling = shape, blocksize, scaling
+        if fused:
+            y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
+                             lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
+        else:
+            w = dequantize_4bit(packed, absmax=absmax, blocksize=blocksize, dtype=x.dtype, shape=shape)
+            y = F.linear(x, w, bias.to(x.dtype) if bias is not None else None)
+            del w
+            if t is not None:
+                y = y + (t @ lora_b.to(x.dtype).t()).reshape(y.shape)
+        ctx.shape, ctx.blocksize, ctx.scaling, ctx.fused = shape, blocksize, scaling, fused
         ctx.has_bias_grad = bias is not None and bias.requires_grad
         ctx.save_for_backward(x if lora_a is not None else None, packed, absmax, lora_a, lora_b, t)
         return y
@@ -50,8 +79,15 @@ class _NF4LinearFn(torch.autograd.Function):
             u = (dy2 @ lora_b.to(dy2.dtype)) * ctx.scaling                  # [M, R]
         dx = None
         if ctx.needs_input_grad[0]:
-            dx = nf4_gemm_bwd_dx(dy2, packed, absmax, ctx.shape, ctx.blocksize, lora_u=u,
-                                 lora_at=lora_a.t().contiguous().to(dy2.dtype) if lora_a is not None else None)
+            if ctx.fused:
+                dx = nf4_gemm_bwd_dx(dy2, packed, absmax, ctx.shape, ctx.blocksize, lora_u=u,
+                                     lora_at=lora_a.t().contiguous().to(dy2.dtype) if lora_a is not None else None)
+            else:
+                w = dequantize_4bit(packed, absmax=absmax, blocksize=ctx.blocksize, dtype=dy2.dtype, shape=ctx.shape)
+                dx = dy2 @ w
+                del w
+                if u is not None:
+                    dx = dx + u @ lora_a.to(dy2.dtype)
             dx = dx.reshape(*dy.shape[:-1], K)
         d_bias = dy2.sum(0).to(dy.dtype) if ctx.has_bias_grad else None
         d_a = d_b = None
@@ -61,7 +97,7 @@ class _NF4LinearFn(torch.autograd.Function):
                 d_a = (u.t() @ x2).to(lora_a.dtype)                         # [R, K]
             if ctx.needs_input_grad[7]:
                 d_b = (dy2.t() @ t).to(lora_b.dtype)                        # [N, R]
-        return dx, None, None, None, None, d_bias, d_a, d_b, None
+        return dx, None, None, None, None, d_bias, d_a, d_b, None, None
 
 
 def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None,
@@ -71,9 +107,11 @@ def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState
     N, K = shape
     bs = quant_state.blocksize
     rank = lora_a.shape[0] if lora_a is not None else 0
-    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and fused_supported(N, K, bs, backward=True)
-            and rank % 16 == 0):
-        return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling)
+    if x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and rank % 16 == 0:
+        rows = x.numel() // max(K, 1)
+        limit = fused_max_rows()
+        fused = fused_supported(N, K, bs, backward=True) and (limit < 0 or rows <= limit)
+        return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling, fused)
     # unfused GPU path: dequantize into a temporary, then the library GEMM
     w = dequantize_4bit(quantized, quant_state, dtype=x.dtype)
     y = F.linear(x, w, bias.to(x.dtype) if bias is not None else None)

@@ -146,10 +146,17 @@ def test_cache_roundtrip_and_from_cache(cuda, tmp_path):
     np.testing.assert_array_equal(bits16(m3.q_proj.weight).ravel(), oracle_dequant_bits(w_q))
 
 
+# NF4Linear picks the fused kernels up to STRATUM_NF4_FUSED_MAX_ROWS rows and
+# dequantize + library GEMM above; both paths are checked at the same sizes.
+PATHS = {"fused": "-1", "library": "0"}
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_nf4_linear_forward_backward(cuda, dtype):
+def test_nf4_linear_forward_backward(cuda, dtype, path, monkeypatch):
     from stratum_amd.functional import quantize_4bit
     from stratum_amd.nf4_linear import NF4Linear
+    monkeypatch.setenv("STRATUM_NF4_FUSED_MAX_ROWS", PATHS[path])
     N, K, M = 384, 256, 200
     w = seeded((N, K), 5, 0.02, torch.float16)
     q, st = quantize_4bit(w.to(cuda))
@@ -170,9 +177,11 @@ def test_nf4_linear_forward_backward(cuda, dtype):
     assert ((x.grad.float() - xr.grad).norm() / xr.grad.norm()).item() <= tol
 
 
-def test_nf4_lora_linear_gradients(cuda):
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_nf4_lora_linear_gradients(cuda, path, monkeypatch):
     from stratum_amd.functional import quantize_4bit
     from stratum_amd.nf4_linear import NF4LoRALinear
+    monkeypatch.setenv("STRATUM_NF4_FUSED_MAX_ROWS", PATHS[path])
     dtype = torch.bfloat16
     N, K, M, r = 512, 256, 160, 16
     w = seeded((N, K), 15, 0.02, torch.float16)
@@ -228,3 +237,27 @@ def test_layer_stream_materialises_each_layer_then_frees_it(cuda):
     for i, layer in NF4LayerStream(layers, 0, free_after=False):
         np.testing.assert_array_equal(bits16(layer.weight).ravel(), refs[i])
     assert all(l.weight.numel() == 384 * 256 for l in layers)
+
+
+def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
+    """Default threshold: 512 rows fused, 513 rows through the library GEMM; both
+    agree with the fp32 reference."""
+    import importlib
+    from stratum_amd.functional import quantize_4bit
+    NL = importlib.import_module("stratum_amd.nf4_linear")  # the package exports a function of that name
+    monkeypatch.delenv("STRATUM_NF4_FUSED_MAX_ROWS", raising=False)
+    assert NL.fused_max_rows() == 512
+    N, K = 256, 128
+    w = seeded((N, K), 21, 0.02, torch.float16)
+    q, st = quantize_4bit(w.to(cuda))
+    st.dtype = torch.bfloat16
+    wq = oracle_weight(w, torch.bfloat16, cuda)
+    calls = []
+    real = NL._NF4LinearFn.apply
+    monkeypatch.setattr(NL._NF4LinearFn, "apply", lambda *a: calls.append(a[-1]) or real(*a))
+    for M in (512, 513):
+        x = seeded((M, K), 22, 1.0, torch.bfloat16).to(cuda)
+        y = NL.NF4Linear(q, st)(x)
+        ref = x.float() @ wq.t().contiguous()
+        assert ((y.float() - ref).norm() / ref.norm()).item() <= 1e-2
+    assert calls == [True, False]

@@ -96,14 +96,16 @@ def _oracle_weights(dense, dtype, device):
     return out
 
 
+@pytest.mark.parametrize("chunk", [96, 300])  # 192 rows per chunk: fused kernels; 600: library GEMM
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_nf4_memory_flat_mlp_matches_fp32_reference(cuda, dtype):
+def test_nf4_memory_flat_mlp_matches_fp32_reference(cuda, dtype, chunk, monkeypatch):
     from stratum_amd.mlp import MemoryFlatFrozenMLP, _STACK_ATTR, quantize_mlp_
+    monkeypatch.delenv("STRATUM_NF4_FUSED_MAX_ROWS", raising=False)
     H, I = 1024, 3072
     dense = DenseMlp(H, I, dtype, cuda, seed=5)
     W = _oracle_weights(dense, dtype, cuda)
     mlp = quantize_mlp_(dense)
-    wrapped = MemoryFlatFrozenMLP(mlp, token_chunk_size=96)
+    wrapped = MemoryFlatFrozenMLP(mlp, token_chunk_size=chunk)
     g = torch.Generator().manual_seed(9)
     x0 = torch.randn(2, 300, H, generator=g).to(dtype).to(cuda)
     x = x0.clone().requires_grad_(True)
