@@ -19,13 +19,23 @@ namespace stm {
 template <int DT>
 using Tr16 = std::conditional_t<DT == STM_BF16, BF16, F16>;
 
-__device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
+// max that propagates NaN (IEEE 754-2019 maximum: v_maximum3_f32 on gfx950,
+// which also takes |x| as a free source modifier) -- a block holding a NaN has
+// a NaN absmax, as torch.max gives the reference.
+__device__ __forceinline__ float nanmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// clamp to [-1, 1] (NaN -> -1, which the table maps to code 0 like both rules do)
+// Level of s = x / absmax. s is clamped to [-1, 1] (v_med3_f32: +-inf from an
+// absmax whose reciprocal overflows go to +-1, as the CPU rule's clamp does);
+// cell j = (int)(c * 32 + 32) in [0, 64] (c * 32 is exact, so the fma rounds
+// once, like the multiply-then-add the table was built for), converted with
+// v_cvt_i32_f32, which maps NaN to 0. A NaN s (all-zero or NaN block) thus
+// reaches cell 0, whose base is code 0 and whose bound (2.0) is never met --
+// code 0, as both bitsandbytes rules give -- whether v_med3 returns the NaN or -1.
 __device__ __forceinline__ uint32_t level_of(float s, const float* __restrict__ bound,
                                              const uint32_t* __restrict__ base) {
-    float c = (s >= -1.0f) ? ((s <= 1.0f) ? s : 1.0f) : -1.0f;
-    int j = (int)(c * 32.0f + 32.0f);
+    const float c = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
+    int j;
+    __asm__("v_cvt_i32_f32 %0, %1" : "=v"(j) : "v"(__builtin_fmaf(c, 32.0f, 32.0f)));
     return base[j] + (c >= bound[j] ? 1u : 0u);
 }
 
@@ -57,40 +67,51 @@ __device__ __forceinline__ void load8(const void* __restrict__ x, int64_t g, flo
 }
 
 // L lanes per quantization block, C 8-element chunks per lane: blocksize = 8 * L * C.
-template <int DT, int L, int C>
+// A wave handles U rounds of 64 / L consecutive blocks. All its loads are
+// issued first (U * C 16-byte loads per lane in flight), then the cell table
+// is copied to LDS -- so the table setup and the barrier overlap the HBM
+// latency -- and then each round is reduced, quantized and stored. Every
+// thread reaches the barrier; rounds past the end are masked.
+template <int DT, int L, int C, int U>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
                                                   float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
     __shared__ float s_bound[65];
     __shared__ uint32_t s_base[65];
+    constexpr int BPW = 64 / L;  // blocks per round
+    constexpr int GPB = L * C;   // 8-element groups per block
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+    const int64_t first = wave * (BPW * U);
+
+    float v[U][C][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t blk = first + u * BPW + lane / L;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            if (blk < nblocks) {
+                load8<DT>(x, blk * GPB + c * L + (lane % L), v[u][c]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[u][c][e] = 0.0f;
+            }
+        }
+    }
     if (threadIdx.x < 65) {
         s_bound[threadIdx.x] = tab.bound[threadIdx.x];
         s_base[threadIdx.x] = tab.base[threadIdx.x];
     }
     __syncthreads();
 
-    constexpr int BPW = 64 / L;       // blocks per wave iteration
-    constexpr int GPB = L * C;        // 8-element groups per block
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
-    const int64_t nwaves = (int64_t)gridDim.x * 4;
-
-    for (int64_t b0 = wave * BPW; b0 < nblocks; b0 += nwaves * BPW) {
-        const int64_t blk = b0 + lane / L;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t blk = first + u * BPW + lane / L;
         const bool active = blk < nblocks;
-        float v[C][8];
         float a = 0.0f;
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-            const int64_t g = blk * GPB + c * L + (lane % L);
-            if (active) {
-                load8<DT>(x, g, v[c]);
-            } else {
+        for (int c = 0; c < C; ++c)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[c][e] = 0.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a = nanmax(a, fabsf(v[c][e]));
-        }
+            for (int e = 0; e < 8; ++e) a = nanmax(a, fabsf(v[u][c][e]));
 #pragma unroll
         for (int off = 1; off < L; off <<= 1) a = nanmax(a, __shfl_xor(a, off));
         const float r = 1.0f / a;  // IEEE division (correctly rounded)
@@ -99,8 +120,8 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, ui
             uint32_t word = 0;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                uint32_t q0 = level_of(v[c][2 * p] * r, s_bound, s_base);
-                uint32_t q1 = level_of(v[c][2 * p + 1] * r, s_bound, s_base);
+                uint32_t q0 = level_of(v[u][c][2 * p] * r, s_bound, s_base);
+                uint32_t q1 = level_of(v[u][c][2 * p + 1] * r, s_bound, s_base);
                 word |= ((q0 << 4) | q1) << (8 * p);
             }
             if (active) packed[blk * GPB + c * L + (lane % L)] = word;
@@ -135,28 +156,32 @@ __global__ __launch_bounds__(64) void k_quantize_generic(const void* __restrict_
     }
 }
 
+template <int DT, int L, int C, int U>
+static void quantize_launch(const void* A, int64_t nfull, const CellTable& tab, uint32_t* p4, float* absmax,
+                            hipStream_t stream) {
+    const int64_t per_wave = (64 / L) * U;
+    const int64_t waves = (nfull + per_wave - 1) / per_wave;
+    const int64_t grid = (waves + 3) / 4;
+    hipLaunchKernelGGL((k_quantize<DT, L, C, U>), dim3((unsigned)grid), dim3(256), 0, stream, A, p4, absmax, nfull,
+                       tab);
+}
+
 template <int DT>
-static void quantize_vec_dispatch(const void* A, int64_t nfull, int bs, const CellTable& tab, uint8_t* packed,
-                                  float* absmax, hipStream_t stream) {
-    // one wave handles 64/L blocks per iteration; one iteration per wave keeps
-    // every load in flight at once (grid-stride beyond 2^20 work-groups)
-    const int L = bs >= 512 ? 64 : bs / 8;
-    const int64_t per_wave = 64 / L;
-    int64_t waves = (nfull + per_wave - 1) / per_wave;
-    int64_t grid = (waves + 3) / 4;
-    if (grid < 1) grid = 1;
-    if (grid > (1 << 20)) grid = 1 << 20;
+static int quantize_vec_dispatch(const void* A, int64_t nfull, int bs, const CellTable& tab, uint8_t* packed,
+                                 float* absmax, hipStream_t stream) {
+    // one work-group = 4 waves; a wave covers U * 64 / L blocks
+    if ((nfull + 3) / 4 > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "quantize: n too large");
     uint32_t* p4 = reinterpret_cast<uint32_t*>(packed);
-    dim3 g((unsigned)grid), b(256);
     switch (bs) {
-        case 64: hipLaunchKernelGGL((k_quantize<DT, 8, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        case 128: hipLaunchKernelGGL((k_quantize<DT, 16, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        case 256: hipLaunchKernelGGL((k_quantize<DT, 32, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        case 512: hipLaunchKernelGGL((k_quantize<DT, 64, 1>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        case 1024: hipLaunchKernelGGL((k_quantize<DT, 64, 2>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        case 2048: hipLaunchKernelGGL((k_quantize<DT, 64, 4>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
-        default: hipLaunchKernelGGL((k_quantize<DT, 64, 8>), g, b, 0, stream, A, p4, absmax, nfull, tab); break;
+        case 64: quantize_launch<DT, 8, 1, 4>(A, nfull, tab, p4, absmax, stream); break;
+        case 128: quantize_launch<DT, 16, 1, 4>(A, nfull, tab, p4, absmax, stream); break;
+        case 256: quantize_launch<DT, 32, 1, 4>(A, nfull, tab, p4, absmax, stream); break;
+        case 512: quantize_launch<DT, 64, 1, 4>(A, nfull, tab, p4, absmax, stream); break;
+        case 1024: quantize_launch<DT, 64, 2, 2>(A, nfull, tab, p4, absmax, stream); break;
+        case 2048: quantize_launch<DT, 64, 4, 1>(A, nfull, tab, p4, absmax, stream); break;
+        default: quantize_launch<DT, 64, 8, 1>(A, nfull, tab, p4, absmax, stream); break;
     }
+    return STM_OK;
 }
 
 int launch_quantize(const void* A, int dtype, int64_t n, int bs, const CellTable& tab, uint8_t* packed,
@@ -165,13 +190,14 @@ int launch_quantize(const void* A, int dtype, int64_t n, int bs, const CellTable
     const bool vec_ok = aligned(A, 16) && aligned(packed, 4);
     const int64_t nfull = vec_ok ? n / bs : 0;
     if (nfull > 0) {
+        int rc;
         if (dtype == STM_F16)
-            quantize_vec_dispatch<STM_F16>(A, nfull, bs, tab, packed, absmax, stream);
+            rc = quantize_vec_dispatch<STM_F16>(A, nfull, bs, tab, packed, absmax, stream);
         else if (dtype == STM_BF16)
-            quantize_vec_dispatch<STM_BF16>(A, nfull, bs, tab, packed, absmax, stream);
+            rc = quantize_vec_dispatch<STM_BF16>(A, nfull, bs, tab, packed, absmax, stream);
         else
-            quantize_vec_dispatch<STM_F32>(A, nfull, bs, tab, packed, absmax, stream);
-        int rc = check_launch("quantize");
+            rc = quantize_vec_dispatch<STM_F32>(A, nfull, bs, tab, packed, absmax, stream);
+        if (rc == STM_OK) rc = check_launch("quantize");
         if (rc) return rc;
     }
     if (nfull < nblocks) {

@@ -74,6 +74,36 @@ def test_quantize_bit_exact(cuda, rule, dtype, shape, bs):
     np.testing.assert_array_equal(packed.cpu().numpy().ravel(), ref_p)
 
 
+@pytest.mark.parametrize("rule", ["argmin", "threshold"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_quantize_special_blocks_bit_exact(cuda, rule, dtype):
+    """Blocks holding NaN, +-inf, only zeros (with -0.0), a subnormal absmax
+    whose reciprocal overflows (bf16/fp32), values of both signs at exactly
+    +-absmax, and an ordinary block -- codes bit-exact and absmax equal (NaN
+    where the oracle has NaN) against the C oracle."""
+    from stratum_amd.functional import quantize_4bit
+    bs = 64
+    blocks = []
+    g = torch.Generator().manual_seed(77)
+    base = torch.randn(bs, generator=g) * 0.02
+    b = base.clone(); b[5] = float("nan"); blocks.append(b)
+    b = base.clone(); b[9] = float("inf"); blocks.append(b)
+    b = base.clone(); b[17] = float("-inf"); blocks.append(b)
+    b = torch.zeros(bs); b[::3] = -0.0; blocks.append(b)
+    tiny = {torch.float16: 6e-8, torch.bfloat16: 1e-39, torch.float32: 1e-40}[dtype]
+    b = torch.zeros(bs); b[::2] = tiny; b[1::4] = -tiny; blocks.append(b)
+    b = base.clone(); b[0] = b.abs().max() * 2; b[1] = -b[0]; blocks.append(b)
+    b = base.clone(); b[2] = float("nan"); b[3] = float("inf"); blocks.append(b)
+    blocks.append(base.clone())
+    x = torch.cat(blocks).to(dtype)
+    packed, state = quantize_4bit(x.to(cuda), blocksize=bs, rounding=rule)
+    ref_p, ref_a = oracle_quant(x, bs, rule)
+    np.testing.assert_array_equal(packed.cpu().numpy().ravel(), ref_p)
+    got = state.absmax.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref_a))
+    np.testing.assert_array_equal(got[~np.isnan(got)].view(np.uint32), ref_a[~np.isnan(ref_a)].view(np.uint32))
+
+
 def test_quantize_unaligned_input_and_cpu_input(cuda):
     from stratum_amd import _lib
     from stratum_amd.functional import quantize_4bit
