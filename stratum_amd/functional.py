@@ -38,10 +38,27 @@ ROUNDING_RULES = {"argmin": _lib.STM_NF4_ARGMIN, "threshold": _lib.STM_NF4_THRES
 DEFAULT_ROUNDING = "argmin"
 
 
+_CODE_ON_DEVICE: dict = {}
+
+
 def get_4bit_type(typename: str = "nf4", device=None) -> torch.Tensor:
+    """The 16 NF4 levels as an fp32 tensor on ``device``.
+
+    On a GPU one tensor per device is created once and shared by every
+    QuantState (a fresh host-to-device copy per quantize call would block the
+    host); treat it as read-only.
+    """
     if typename != "nf4":
         raise NotImplementedError(f"4-bit type {typename!r} is not supported (only 'nf4')")
-    return torch.tensor(NF4_LEVELS, dtype=torch.float32, device=device)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    if dev.type != "cuda":
+        return torch.tensor(NF4_LEVELS, dtype=torch.float32, device=dev)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    code = _CODE_ON_DEVICE.get(dev)
+    if code is None:
+        code = _CODE_ON_DEVICE[dev] = torch.tensor(NF4_LEVELS, dtype=torch.float32, device=dev)
+    return code
 
 
 class QuantState:

@@ -339,3 +339,38 @@ def test_grouped_gemm_matches_per_expert_reference(cuda, dtype):
             continue
         assert _rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype]
         assert _rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype]
+
+
+def test_entry_points_replay_correctly_in_a_hip_graph(cuda):
+    """quantize, dequantize and a split-reduction GEMM (M = 16) captured into
+    one HIP graph: every replay, with eager work and synchronisations between
+    replays, matches the eager results bit for bit. (The entry points record no
+    memset: the split partials are fully overwritten.)"""
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_fwd, quantize_4bit
+    w = seeded((1024, 2048), 91, 0.02, torch.float16).to(cuda)
+    x = seeded((16, 2048), 92, 1.0, torch.bfloat16).to(cuda)
+    p_e, s_e = quantize_4bit(w)
+    d_e = dequantize_4bit(p_e, s_e, dtype=torch.bfloat16)
+    y_e = nf4_gemm_fwd(x, p_e, s_e.absmax, (1024, 2048), 64)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        quantize_4bit(w)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        p_g, s_g = quantize_4bit(w)
+        d_g = dequantize_4bit(p_g, s_g, dtype=torch.bfloat16)
+        y_g = nf4_gemm_fwd(x, p_g, s_g.absmax, (1024, 2048), 64)
+    for i in range(3):
+        # eager work between replays that touches the same kind of kernels
+        junk = nf4_gemm_fwd(x.flip(0), p_e, s_e.absmax, (1024, 2048), 64)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(p_g, p_e), i
+        assert torch.equal(s_g.absmax, s_e.absmax), i
+        assert torch.equal(d_g, d_e), i
+        assert torch.equal(y_g, y_e), i
+        del junk
