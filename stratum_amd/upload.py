@@ -683,3 +683,9 @@ def _build_param_owner_map(module: torch.nn.Module) -> dict:
 def nf4_code_table(device=None) -> torch.Tensor:
     """The fp32 [16] NF4 level table stored in ``NF4Payload.code``."""
     return get_4bit_type("nf4", device=device)
+
+
+# Checkpoint loaders (stratum/upload.py:425-904,1325-1440) live in .checkpoint;
+# imported last because they use this module's helpers.
+from .checkpoint import (_build_ckpt_key_fn, _try_load_fused_experts, load_module_fp16_from_checkpoint,  # noqa: E402
+                         populate_from_hf_checkpoint, stream_load_and_quantize_module)

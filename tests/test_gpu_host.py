@@ -261,3 +261,41 @@ def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
         ref = x.float() @ wq.t().contiguous()
         assert ((y.float() - ref).norm() / ref.norm()).item() <= 1e-2
     assert calls == [True, False]
+
+
+def test_stream_load_and_quantize_from_checkpoint_bit_exact(cuda, tmp_path):
+    """Cold build straight from a safetensors checkpoint: every eligible weight is
+    quantized by the GPU kernel; payload codes/absmax and the later ensure_weights
+    dequantization are bit-exact against the oracle; the cache written on the way
+    serves a second build."""
+    from safetensors.torch import save_file
+    from stratum_amd.upload import NF4_ATTR, ensure_weights, stream_load_and_quantize_module
+    w = seeded((512, 256), 31, 0.02, torch.float16)
+    norm = seeded((512,), 32, 1.0, torch.float16)
+    save_file({"model.layers.0.proj.weight": w, "model.layers.0.norm": norm}, str(tmp_path / "model.safetensors"))
+
+    class M(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = nn.Module()
+            self.model.layers = nn.ModuleList([nn.Module()])
+            lay = self.model.layers[0]
+            lay.proj = nn.Linear(256, 512, bias=False, device="meta", dtype=torch.float16)
+            lay.norm = nn.Parameter(torch.empty(512, device="meta", dtype=torch.float16))
+            for p in self.parameters():
+                p.requires_grad_(False)
+
+    m = M()
+    stats = stream_load_and_quantize_module(m, str(tmp_path), cache_dir=tmp_path / "cache")
+    assert stats is not None and stats.tensors == 1 and stats.cache_writes == 1
+    pl = getattr(m.model.layers[0].proj.weight, NF4_ATTR)
+    ref_p, ref_a = C.quantize(bits16(w), O.DT_F16, 64, "argmin")
+    np.testing.assert_array_equal(pl.quantized.numpy().ravel(), ref_p)
+    np.testing.assert_array_equal(pl.absmax.numpy().view(np.uint32), ref_a.view(np.uint32))
+    assert pl.quantized.is_pinned()
+    assert ensure_weights(m, 0) >= 1
+    np.testing.assert_array_equal(bits16(m.model.layers[0].proj.weight).ravel(), oracle_dequant_bits(w))
+    assert torch.equal(m.model.layers[0].norm.cpu(), norm)
+    m2 = M()
+    stats2 = stream_load_and_quantize_module(m2, str(tmp_path), cache_dir=tmp_path / "cache")
+    assert stats2.cache_hits == 1
