@@ -236,9 +236,9 @@ def run_lora_step(args):
         "data": "synthetic (seeded N(0,0.02) fp16 weight quantized to NF4, N(0,1) bf16 activations)",
         "config": {"workload": "lora_step_nf4_w14336x4096_x8192", "M": M, "N": N, "K": K, "lora_rank": R,
                    "blocksize": 64, "parallelism": "single-gpu"},
-        "roofline": {"bound": "mfma", "kernel": "k_gemm_fwd<BF16>", "achieved": round(fwd_tf, 2),
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_fwd_rw<BF16>", "achieved": round(fwd_tf, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd"),
+                     "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd_rw"),
                      "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
         "bwd_dx": {"kernel": "k_gemm_bwd<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},

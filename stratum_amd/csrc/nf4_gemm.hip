@@ -92,6 +92,16 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
     __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
                      : "memory", "m0");
 }
+// The same copy from a wave-uniform 64-bit base plus a 32-bit per-lane byte offset
+// (global_load_lds with an SGPR base: no 64-bit address arithmetic per copy).
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_t lds_base) {
+    const uint64_t b = (uint64_t)(size_t)base;
+    const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const void* sbase = (const void*)(size_t)sb;
+    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
+                     : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima). Emitted through the
@@ -170,6 +180,36 @@ struct ActStage {
     }
 };
 
+// ActStage with a wave-uniform base and 32-bit byte offsets (the tile's rows
+// must lie within 4 GiB of the base).
+template <int BM, int NW>
+struct ActStageS {
+    static constexpr int XI = BM / (8 * NW);
+    const uint16_t* base;
+    uint32_t off[XI];
+    uint32_t lds[2][XI];
+
+    __device__ __forceinline__ void init(const uint16_t* b, int64_t ld, int64_t m0, int64_t rows, const uint4* buf0,
+                                         const uint4* buf1, int wave, int lane) {
+        base = b;
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int r0 = (wave * XI + i) * 8;
+            const int r = r0 + (lane >> 3);
+            const int c = (lane & 7) ^ swz_key(r);
+            int64_t row = m0 + r;
+            row = row < rows ? row : rows - 1;
+            off[i] = (uint32_t)((row * ld + c * 8) * 2);
+            lds[0][i] = __builtin_amdgcn_readfirstlane(lds_offset(buf0 + r0 * 8));
+            lds[1][i] = __builtin_amdgcn_readfirstlane(lds_offset(buf1 + r0 * 8));
+        }
+    }
+    __device__ __forceinline__ void issue(int64_t k0, int buf) const {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) dma16_s(base + k0, off[i], lds[buf][i]);
+    }
+};
+
 // Level table: entry (byte b, copy c) = (level[b >> 4], level[b & 15]) at
 // index 16 b + c. Lane l reads copy l % 16, so the 16 lanes of one LDS pass of
 // a 64-bit read always hit 16 different bank pairs (a single shared copy makes
@@ -232,13 +272,16 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FA][FB], uint16
         uint16_t* dst = out + orow * ld;
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
+            // one fragment at a time out of the accumulator registers
+            f32x16_t a = acc[i][j];
+            __asm__ volatile("" : "+v"(a));
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t col = ocol_base + i * 32 + 8 * q + 4 * (lane >> 5);
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[e] = acc[i][j][4 * q + e];
+                    v[e] = a[4 * q + e];
                     if (bias && col + e < ocols) v[e] += Tr::to_f32(bias[col + e]);
                 }
                 if (col + 3 < ocols) {
@@ -450,16 +493,24 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     const int wm = wave / WN, wn = wave % WN;
     fill_lut<NT>(lut_all, tid);
 
-    const Group grp = group_of(g, blockIdx.y);
     const int64_t K = g.K, N = g.N;
-    const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
+    const int64_t work = tiles * g.num_groups * g.splits;
+    // Work item w = (tile, group, split); a work-group takes items w, w + grid, ...
+    // (one item each when the grid covers them all, else a persistent loop that
+    // fills the level table once and overlaps one item's stores with the next
+    // item's first loads).
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
+    const int64_t rest = w / tiles;
+    const int z = (int)(rest / g.num_groups);
+    const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tn;
-    tile_coords(blockIdx.x, ntm, ntn, tm, tn);
+    tile_coords(w % tiles, ntm, ntn, tm, tn);
     const int64_t m0 = tm * BM, n0 = tn * BN;
-    if (m0 >= grp.rows) return;
+    if (m0 >= grp.rows) continue;  // uniform over the work-group
 
     int s_begin, KT;
-    split_range((int)(K / BK), g.splits, blockIdx.z, s_begin, KT);
+    split_range((int)(K / BK), g.splits, z, s_begin, KT);
     const uint16_t* __restrict__ X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K + (int64_t)s_begin * BK;
     const int64_t kblocks = K / g.blocksize;
 
@@ -482,16 +533,301 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, X, K, m0, grp.rows, KT, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = n0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
-    if (g.lora_rank > 0 && blockIdx.z == 0)
+    if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
                               grp.rows, g.lora_rank, lane);
     if (g.splits > 1)
-        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)blockIdx.z * g.M * N, N, col_base, N, row_base, grp.rows,
-                               lane);
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * N, N, col_base, N, row_base, grp.rows, lane);
     else
         store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, col_base, N, row_base,
                                grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane);
+    __syncthreads();  // all waves are done with the LDS buffers before the next item fills them
+    }
+}
+
+// ------------------------------------------------- forward, register weights
+// Y tile BM x 256 with 4 WM waves; wave (wm, wn) owns the 64 output columns
+// [n0 + 64 wn, n0 + 64 wn + 64) over rows [m0 + wm BM / WM, ...) (2 x BM/WM/32
+// MFMA tiles; 256 accumulators per lane for BM = 256, WM = 1, the product
+// configuration). Because no two waves along N share a weight column, each wave
+// dequantizes its weight fragments straight into MFMA operand registers: the
+// weight never goes through LDS, only the activation tile (shared by the waves)
+// and the level table do. Launched for unsplit, single-matrix problems.
+//
+// Reduction order inside a 64-deep step: lane half h = lane / 32 of a weight row
+// loads the 16 packed bytes of k in [32 h, 32 h + 32); MFMA sub-step j takes
+// packed word j, i.e. k = 32 h + 8 j + (0..7). The activation operand of lane
+// (row, h) at sub-step j is the 16-byte LDS chunk 4 h + j of its row -- the same
+// k set, so the product is the plain dot product over the step.
+//
+// Step s (activation buffers alternate): copy the activation tile of step s + 1
+// into the other LDS buffer and fetch the packed weights of step s + 2 into
+// VGPRs; run sub-steps 0..2 on operands already in registers; wait for the
+// copies, barrier; run sub-step 3, whose operands were read before the barrier,
+// while the first activation fragments of step s + 1 are read. Each sub-step
+// reloads every activation fragment in place right after its two MFMAs, and
+// rewrites one weight-fragment slot just after the slot's MFMAs (the table reads
+// for it issued one sub-step earlier), so neither operand is double-buffered
+// (32 + 32 VGPRs for BM = 256). sched_group_barrier interleaves each
+// sub-step as 2 VALU, 1 LDS read, 1 MFMA per slot; with one wave per SIMD, work
+// that is not interleaved with MFMAs leaves the matrix core idle.
+
+// Level table for the register-weight kernel: entry (byte b, copy c) at
+// float2 index 32 b + c, so the LDS byte address of a lookup is
+// (b << 8) | (8 c), one v_perm_b32 from the packed word and the lane's copy
+// offset; lanes 0..31 of a pass read 32 different copies (all 64 banks).
+constexpr int RW_LUT_COPIES = 32;
+
+template <int NT>
+__device__ __forceinline__ void fill_lut_rw(float2* lut, int tid) {
+    for (int t = tid; t < 256 * RW_LUT_COPIES; t += NT) {
+        const int b = t / RW_LUT_COPIES;
+        lut[t] = make_float2(kLevelsDev[b >> 4], kLevelsDev[b & 15]);
+    }
+}
+
+template <typename Tr>
+struct RwWeights {
+    struct Raw {
+        uint4 q[2];
+        float a[2];
+    };
+    const uint8_t* packed;  // the group's packed weight
+    const float* absmax;    // the group's absmax
+    uint32_t woff[2];       // byte offset of this lane's 16-byte run of the first step, fragment i
+    uint32_t aoff[2];       // absmax index of the start of weight row (fragment i)
+    int bshift;
+    uint32_t lut_base;     // LDS byte address of the level table
+    uint32_t copy_off;     // 8 * (lane % 32)
+
+    __device__ __forceinline__ void load(int64_t k0, Raw& r) const {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            r.q[i] = *reinterpret_cast<const uint4*>(packed + (woff[i] + (uint32_t)(k0 / 2)));
+            r.a[i] = absmax[aoff[i] + (uint32_t)(k0 >> bshift)];
+        }
+    }
+    __device__ __forceinline__ static uint32_t word(const uint4& q, int j) {
+        return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    }
+    // table reads for sub-step j of both fragments (8 lookups)
+    __device__ __forceinline__ void issue(const Raw& r, int j, f32x2_t (&p)[2][4]) const {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t x = word(r.q[i], j);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                // bytes: [0] = copy offset, [1] = packed byte b of x, [2], [3] = 0
+                const uint32_t addr = __builtin_amdgcn_perm(copy_off, x, 0x0C0C0004u | ((uint32_t)b << 8));
+                p[i][b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)(lut_base + addr);
+            }
+        }
+    }
+    __device__ __forceinline__ static void finish(const Raw& r, const f32x2_t (&p)[2][4], uint4 (&out)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float a = r.a[i];
+            out[i].x = Tr::pack2(opaque(p[i][0].x * a), opaque(p[i][0].y * a));
+            out[i].y = Tr::pack2(opaque(p[i][1].x * a), opaque(p[i][1].y * a));
+            out[i].z = Tr::pack2(opaque(p[i][2].x * a), opaque(p[i][2].y * a));
+            out[i].w = Tr::pack2(opaque(p[i][3].x * a), opaque(p[i][3].y * a));
+        }
+    }
+};
+
+template <int FB>
+__device__ __forceinline__ void read_x(uint4 (&x)[FB], const uint4* sx, int xrow0, int lane, int j) {
+    const int ch = 4 * (lane >> 5) + j;
+#pragma unroll
+    for (int f = 0; f < FB; ++f) x[f] = sx[swz(xrow0 + f * 32 + (lane & 31), ch)];
+}
+
+// MFMAs of one sub-step; each activation fragment is reloaded in place with
+// the fragment of sub-step jn (from buffer sx) once its two MFMAs are issued.
+template <typename Tr, int FB>
+__device__ __forceinline__ void mma_sub(f32x16_t (&acc)[2][FB], const uint4 (&w)[2], uint4 (&x)[FB],
+                                        const uint4* sx, int xrow0, int lane, int jn) {
+    const int ch = 4 * (lane >> 5) + jn;
+#pragma unroll
+    for (int f = 0; f < FB; ++f) {
+        acc[0][f] = mfma<Tr>(w[0], x[f], acc[0][f]);
+        acc[1][f] = mfma<Tr>(w[1], x[f], acc[1][f]);
+        x[f] = sx[swz(xrow0 + f * 32 + (lane & 31), ch)];
+    }
+}
+
+// store_tile for k_gemm_fwd_rw: 32-bit element offsets from the tile's base
+// (the output has fewer than 2^31 elements), one row offset per fragment row
+// and compile-time column offsets, so few address registers are live.
+template <typename Tr, int FA, int FB>
+__device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
+                                              int ocol_base, int ocols, int orow_base, int orows,
+                                              const uint16_t* __restrict__ bias, int lane) {
+    const int c0 = ocol_base + 4 * (lane >> 5);
+    float bv[FA][4][4];
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int col = c0 + i * 32 + 8 * q + e;
+                bv[i][q][e] = (bias && col < ocols) ? Tr::to_f32(bias[col]) : 0.0f;
+            }
+    const bool full = ocol_base + FA * 32 <= ocols;
+#pragma unroll
+    for (int j = 0; j < FB; ++j) {
+        const int orow = orow_base + j * 32 + (lane & 31);
+        if (orow >= orows) continue;
+        uint16_t* dst = out + (orow * ld + c0);
+#pragma unroll
+        for (int i = 0; i < FA; ++i) {
+            f32x16_t a = acc[i][j];
+            __asm__ volatile("" : "+v"(a));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = a[4 * q + e] + bv[i][q][e];
+                const int dc = i * 32 + 8 * q;
+                if (full) {
+                    uint2 pk;
+                    pk.x = Tr::pack2(v[0], v[1]);
+                    pk.y = Tr::pack2(v[2], v[3]);
+                    *reinterpret_cast<uint2*>(dst + dc) = pk;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c0 + dc + e < ocols) dst[dc + e] = Tr::from_f32(v[e]);
+                }
+            }
+        }
+    }
+}
+
+template <typename Tr, int BM, int WM>
+__global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
+    constexpr int BN = 256, NT = 256 * WM, FB = BM / WM / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave & 3, xrow0 = (wave >> 2) * (BM / WM);
+
+    __shared__ float2 lut_all[256 * RW_LUT_COPIES];
+    __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
+
+    fill_lut_rw<NT>(lut_all, tid);
+
+    const int64_t K = g.K, N = g.N;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
+    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1)
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items as in k_gemm_fwd
+    const Group grp = group_of(g, (int)(w / tiles));
+    int64_t tm, tn;
+    tile_coords(w % tiles, ntm, ntn, tm, tn);
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= grp.rows) continue;
+
+    const int KT = (int)(K / BK);
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K;
+
+    RwWeights<Tr> ws;
+    ws.bshift = 31 - __builtin_clz(g.blocksize);
+    ws.lut_base = (uint32_t)(size_t)((const __attribute__((address_space(3))) float2*)lut_all);
+    ws.copy_off = 8u * (uint32_t)(lane & 31);
+    const int64_t col_base = n0 + wn * 64;
+    ws.packed = grp.packed;
+    ws.absmax = grp.absmax;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int64_t n = col_base + i * 32 + (lane & 31);
+        n = n < N ? n : N - 1;
+        ws.woff[i] = (uint32_t)(n * (K / 2) + 16 * (lane >> 5));
+        ws.aoff[i] = (uint32_t)(n * (K >> ws.bshift));
+    }
+    ActStageS<BM, 4 * WM> as;
+    as.init(X, K, m0, grp.rows, sA0, sA1, wave, lane);
+
+    f32x16_t acc[2][FB];
+    zero_acc(acc);
+
+    // B[j] = weight fragments of sub-step j. Within step s, slot j is rewritten
+    // right after its MFMAs: slot 3 with step s's sub-step 3 (during sub-step
+    // 0), slots 0..2 with step s + 1's (during sub-steps 1..3). The table reads
+    // of each rewrite are issued one sub-step earlier (into pa / pb, in turn).
+    typename RwWeights<Tr>::Raw raw0, raw1;
+    uint4 B[4][2];
+    uint4 x[FB];
+    f32x2_t pa[2][4], pb[2][4];
+
+    // prologue: activation tile 0, packed weights of steps 0 and 1, fragments
+    // of sub-steps 0..2 of step 0, table reads of its sub-step 3
+    ws.load(0, raw0);
+    ws.load(KT > 1 ? BK : 0, raw1);
+    as.issue(0, 0);
+    wait_vmem();
+    __syncthreads();  // level table and activation tile 0 ready
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        ws.issue(raw0, j, pa);
+        RwWeights<Tr>::finish(raw0, pa, B[j]);
+    }
+    ws.issue(raw0, 3, pa);
+    read_x<FB>(x, sA0, xrow0, lane, 0);
+    sched_fence();
+
+    // one sub-step: MFMAs on (w, x) reloading x with sub-step jn from sx, table
+    // reads into p_next, fragments from p_cur (absmax of r_cur) into bout; the
+    // scheduler interleaves them as 2 VALU, 1 LDS read, 1 MFMA per slot
+    auto sub = [&](const uint4 (&w)[2], const uint4* sx, int jn, const typename RwWeights<Tr>::Raw& r_next,
+                   int word_next, f32x2_t (&p_next)[2][4], const typename RwWeights<Tr>::Raw& r_cur,
+                   const f32x2_t (&p_cur)[2][4], uint4 (&bout)[2]) {
+        ws.issue(r_next, word_next, p_next);
+        mma_sub<Tr, FB>(acc, w, x, sx, xrow0, lane, jn);
+        RwWeights<Tr>::finish(r_cur, p_cur, bout);
+#pragma unroll
+        for (int k = 0; k < 2 * FB; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        sched_fence();
+    };
+
+    // step s: rawc holds step s's packed weights (refilled with step s + 2 once
+    // its absmax has been used), rawn step s + 1's
+    auto step = [&](int s, const uint4* sAc, const uint4* sAn, int nbuf, typename RwWeights<Tr>::Raw& rawc,
+                    const typename RwWeights<Tr>::Raw& rawn) {
+        const int s1 = s + 1 < KT ? s + 1 : KT - 1;
+        const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+        as.issue((int64_t)s1 * BK, nbuf);
+        sub(B[0], sAc, 1, rawn, 0, pb, rawc, pa, B[3]);
+        ws.load((int64_t)s2 * BK, rawc);
+        sub(B[1], sAc, 2, rawn, 1, pa, rawn, pb, B[0]);
+        sub(B[2], sAc, 3, rawn, 2, pb, rawn, pa, B[1]);
+        wait_vmem();
+        __syncthreads();  // activation tile s + 1 in sAn; every wave is done reading sAc
+        sub(B[3], sAn, 0, rawn, 3, pa, rawn, pb, B[2]);
+    };
+    int s = 0;
+    for (; s + 1 < KT; s += 2) {
+        step(s, sA0, sA1, 1, raw0, raw1);
+        step(s + 1, sA1, sA0, 0, raw1, raw0);
+    }
+    if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
+
+    // The epilogue's addresses depend only on the tile; an opaque lane index keeps
+    // the compiler from computing them before the main loop and holding (spilling)
+    // them across it.
+    int lane_e = lane;
+    __asm__ volatile("" : "+v"(lane_e));
+    if (g.lora_rank > 0)
+        lora_term<Tr, 2, FB>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
+                             reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0 + xrow0, grp.rows,
+                             g.lora_rank, lane_e);
+    store_tile_rw<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base, (int)N,
+                             (int)(m0 + xrow0), (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane_e);
+    __syncthreads();
+    }
 }
 
 // ----------------------------------------------------------------- backward
@@ -580,16 +916,20 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     const int wm = wave / WN, wn = wave % WN;
     fill_lut<NT>(lut_all, tid);
 
-    const Group grp = group_of(g, blockIdx.y);
     const int64_t K = g.K, N = g.N;
-    const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
+    const int64_t work = tiles * g.num_groups * g.splits;
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items as in k_gemm_fwd
+    const int64_t rest = w / tiles;
+    const int z = (int)(rest / g.num_groups);
+    const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tk;
-    tile_coords(blockIdx.x, ntm, ntk, tm, tk);
+    tile_coords(w % tiles, ntm, ntk, tm, tk);
     const int64_t m0 = tm * BM, k0 = tk * BN;
-    if (m0 >= grp.rows) return;
+    if (m0 >= grp.rows) continue;
 
     int s_begin, NT_steps;
-    split_range((int)(N / BK), g.splits, blockIdx.z, s_begin, NT_steps);
+    split_range((int)(N / BK), g.splits, z, s_begin, NT_steps);
     const uint16_t* __restrict__ DY = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N + (int64_t)s_begin * BK;
     const int64_t kblocks = K / g.blocksize;
     const int bshift = ilog2(g.blocksize);
@@ -611,16 +951,17 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, DY, N, m0, grp.rows, NT_steps, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = k0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
-    if (g.lora_rank > 0 && blockIdx.z == 0)
+    if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
                               grp.rows, g.lora_rank, lane);
     if (g.splits > 1)
-        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)blockIdx.z * g.M * K, K, col_base, K, row_base, grp.rows,
-                               lane);
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * K, K, col_base, K, row_base, grp.rows, lane);
     else
         store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, col_base, K, row_base,
                                grp.rows, nullptr, lane);
+    __syncthreads();
+    }
 }
 
 // Sum of the split partials [splits][rows][cols] (+ bias), one rounding; four
@@ -668,12 +1009,38 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
     return check_launch("gemm split reduce");
 }
 
+#ifndef STM_PERSISTENT
+#define STM_PERSISTENT 1
+#endif
+
+// Compute units of the current device (cached per device): the work-group count
+// of a persistent launch, one work-group per CU (the kernels' LDS allows one).
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+// 1-D grid over the work items (tile, group, split): all of them, or one
+// work-group per CU looping over them.
+dim3 work_grid(int64_t work) {
+    const int64_t cap = STM_PERSISTENT ? (int64_t)device_cus() : work;
+    return dim3((unsigned)(work < cap ? work : cap));
+}
+
 template <int BM, int BN, int WM, int WN>
 int launch_fwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (tiles == 0) return STM_OK;
-    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups, (unsigned)g.splits), block(WM * WN * 64);
+    const int64_t work = tiles * g.num_groups * g.splits;
+    if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
+    dim3 grid = work_grid(work), block(WM * WN * 64);
     if (dtype == STM_BF16)
         hipLaunchKernelGGL((k_gemm_fwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
     else
@@ -685,14 +1052,49 @@ template <int BM, int BN, int WM, int WN>
 int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.K + BN - 1) / BN);
     if (tiles == 0) return STM_OK;
-    if (tiles > 0x7FFFFFFFLL || g.num_groups > 65535)
-        return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)g.num_groups, (unsigned)g.splits), block(WM * WN * 64);
+    const int64_t work = tiles * g.num_groups * g.splits;
+    if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
+    dim3 grid = work_grid(work), block(WM * WN * 64);
     if (dtype == STM_BF16)
         hipLaunchKernelGGL((k_gemm_bwd<BF16, BM, BN, WM, WN>), grid, block, 0, stream, g);
     else
         hipLaunchKernelGGL((k_gemm_bwd<F16, BM, BN, WM, WN>), grid, block, 0, stream, g);
     return check_launch("gemm_bwd_dx");
+}
+
+// The register-weight forward (k_gemm_fwd_rw) replaces the 256 x 256 LDS-weight
+// forward for unsplit single-matrix launches: measured on MI355X 3-4 % faster
+// at M = 512 and 8192 on the 14336 x 4096 and 4096 x 14336 weights. Grouped
+// (expert) launches keep the LDS-weight kernel, which is 5 % faster there
+// (shorter reductions and partly filled tiles). STM_FWD_RW_WM = 2 (eight waves,
+// 128 x 64 wave tiles, the dequantization done twice) measured 14 % slower.
+#ifndef STM_FWD_RW
+#define STM_FWD_RW 1
+#endif
+
+// k_gemm_fwd_rw addresses activations, packed weights and absmax of one group
+// with 32-bit offsets from uniform bases.
+bool rw_offsets_fit(const GemmArgs& g) {
+    const int64_t lim = (int64_t)1 << 32;
+    return g.M * g.K * 2 < lim && g.N * g.K / 2 < lim && g.N * g.K / g.blocksize < lim && g.M * g.N < lim / 2;
+}
+
+#ifndef STM_FWD_RW_WM
+#define STM_FWD_RW_WM 1
+#endif
+
+template <int BM, int WM>
+int launch_fwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
+    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + 255) / 256);
+    if (tiles == 0) return STM_OK;
+    const int64_t work = tiles * g.num_groups;
+    if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
+    dim3 grid = work_grid(work), block(256 * WM);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemm_fwd_rw<BF16, BM, WM>), grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL((k_gemm_fwd_rw<F16, BM, WM>), grid, block, 0, stream, g);
+    return check_launch("gemm_fwd");
 }
 
 }  // namespace
@@ -769,7 +1171,9 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
-    const int rc = p.big ? launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream)
+    const bool rw = STM_FWD_RW && g.splits == 1 && g.num_groups == 1 && !g.offsets && rw_offsets_fit(g);
+    const int rc = p.big ? (rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
+                                       : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream))
                          : launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.N, g.bias, dtype, stream);
