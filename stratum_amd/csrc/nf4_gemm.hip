@@ -272,9 +272,8 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FA][FB], uint16
         uint16_t* dst = out + orow * ld;
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
-            // one fragment at a time out of the accumulator registers
             f32x16_t a = acc[i][j];
-            __asm__ volatile("" : "+v"(a));
+            if constexpr (FA * FB >= 8) __asm__ volatile("" : "+v"(a));  // one fragment at a time out of 128+ accumulators
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t col = ocol_base + i * 32 + 8 * q + 4 * (lane >> 5);
@@ -312,16 +311,17 @@ __device__ __forceinline__ void store_tile_f32(const f32x16_t (&acc)[FA][FB], fl
         float* dst = out + orow * ld;
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
+            f32x16_t a = acc[i][j];
+            if constexpr (FA * FB >= 8) __asm__ volatile("" : "+v"(a));
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t col = ocol_base + i * 32 + 8 * q + 4 * (lane >> 5);
                 if (col + 3 < ocols) {
-                    *reinterpret_cast<float4*>(dst + col) =
-                        make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    *reinterpret_cast<float4*>(dst + col) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (col + e < ocols) dst[col + e] = acc[i][j][4 * q + e];
+                        if (col + e < ocols) dst[col + e] = a[4 * q + e];
                 }
             }
         }
@@ -351,6 +351,15 @@ __device__ __forceinline__ void mma_kk(f32x16_t (&acc)[FA][FB], const uint4* sw,
 }
 
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// An opaque copy of the lane index. Values computed from it stay after the point
+// where it is taken: per-work-item lane offsets are recomputed per item, and
+// epilogue addresses after the main loop, instead of being computed once up
+// front and held (spilled) across the main loop.
+__device__ __forceinline__ int opaque_lane(int lane) {
+    __asm__ volatile("" : "+v"(lane));
+    return lane;
+}
 
 // Shared main loop. Step s computes on buffers (s & 1) while the activation
 // tile of step s + 1 streams into the other LDS buffer, the weight tile of
@@ -489,7 +498,11 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
     __shared__ uint4 sB0[BN * 8], sB1[BN * 8];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (large tiles) the wave index as a uniform value: wave-derived offsets then
+    // live in SGPRs instead of taking VGPRs from the accumulators' neighbours
+    constexpr bool kLargeAcc = (BM / WM / 32) * (BN / WN / 32) >= 8;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = kLargeAcc ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     fill_lut<NT>(lut_all, tid);
 
@@ -533,15 +546,16 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, X, K, m0, grp.rows, KT, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = n0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
+    const int lane_e = FW * FX >= 8 ? opaque_lane(lane) : lane;
     if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
-                              grp.rows, g.lora_rank, lane);
+                              grp.rows, g.lora_rank, lane_e);
     if (g.splits > 1)
-        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * N, N, col_base, N, row_base, grp.rows, lane);
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * N, N, col_base, N, row_base, grp.rows, lane_e);
     else
         store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, N, col_base, N, row_base,
-                               grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane);
+                               grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane_e);
     __syncthreads();  // all waves are done with the LDS buffers before the next item fills them
     }
 }
@@ -709,7 +723,7 @@ __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uin
 template <typename Tr, int BM, int WM>
 __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     constexpr int BN = 256, NT = 256 * WM, FB = BM / WM / 32;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane0 = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 3, xrow0 = (wave >> 2) * (BM / WM);
 
     __shared__ float2 lut_all[256 * RW_LUT_COPIES];
@@ -729,6 +743,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
 
     const int KT = (int)(K / BK);
     const uint16_t* X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K;
+    const int lane = opaque_lane(lane0);
 
     RwWeights<Tr> ws;
     ws.bshift = 31 - __builtin_clz(g.blocksize);
@@ -815,11 +830,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     }
     if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
 
-    // The epilogue's addresses depend only on the tile; an opaque lane index keeps
-    // the compiler from computing them before the main loop and holding (spilling)
-    // them across it.
-    int lane_e = lane;
-    __asm__ volatile("" : "+v"(lane_e));
+    const int lane_e = opaque_lane(lane);
     if (g.lora_rank > 0)
         lora_term<Tr, 2, FB>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
                              reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0 + xrow0, grp.rows,
@@ -912,7 +923,11 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
     __shared__ uint4 sB0[BN * 8], sB1[BN * 8];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (large tiles) the wave index as a uniform value: wave-derived offsets then
+    // live in SGPRs instead of taking VGPRs from the accumulators' neighbours
+    constexpr bool kLargeAcc = (BM / WM / 32) * (BN / WN / 32) >= 8;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = kLargeAcc ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     fill_lut<NT>(lut_all, tid);
 
@@ -951,15 +966,16 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     run_pipeline<Tr, BM, BN, WM, WN, FW, FX>(acc, DY, N, m0, grp.rows, NT_steps, sA0, sA1, sB0, sB1, ws, wave, lane);
 
     const int64_t col_base = k0 + wn * (BN / WN), row_base = m0 + wm * (BM / WM);
+    const int lane_e = FW * FX >= 8 ? opaque_lane(lane) : lane;
     if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, FW, FX>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
                               reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, row_base,
-                              grp.rows, g.lora_rank, lane);
+                              grp.rows, g.lora_rank, lane_e);
     if (g.splits > 1)
-        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * K, K, col_base, K, row_base, grp.rows, lane);
+        store_tile_f32<FW, FX>(acc, g.partial + (int64_t)z * g.M * K, K, col_base, K, row_base, grp.rows, lane_e);
     else
         store_tile<Tr, FW, FX>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, K, col_base, K, row_base,
-                               grp.rows, nullptr, lane);
+                               grp.rows, nullptr, lane_e);
     __syncthreads();
     }
 }
