@@ -567,7 +567,7 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
 // configuration). Because no two waves along N share a weight column, each wave
 // dequantizes its weight fragments straight into MFMA operand registers: the
 // weight never goes through LDS, only the activation tile (shared by the waves)
-// and the level table do. Launched for unsplit, single-matrix problems.
+// and the level table do. Launched for unsplit problems (single-matrix and grouped).
 //
 // Reduction order inside a 64-deep step: lane half h = lane / 32 of a weight row
 // loads the 16 packed bytes of k in [32 h, 32 h + 32); MFMA sub-step j takes
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
 
     const int64_t K = g.K, N = g.N;
     const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
-    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1)
+    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1); items (tile, expert)
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items as in k_gemm_fwd
     const Group grp = group_of(g, (int)(w / tiles));
     int64_t tm, tn;
@@ -1079,11 +1079,12 @@ int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
 }
 
 // The register-weight forward (k_gemm_fwd_rw) replaces the 256 x 256 LDS-weight
-// forward for unsplit single-matrix launches: measured on MI355X 3-4 % faster
-// at M = 512 and 8192 on the 14336 x 4096 and 4096 x 14336 weights. Grouped
-// (expert) launches keep the LDS-weight kernel, which is 5 % faster there
-// (shorter reductions and partly filled tiles). STM_FWD_RW_WM = 2 (eight waves,
-// 128 x 64 wave tiles, the dequantization done twice) measured 14 % slower.
+// forward for unsplit launches, single-matrix and grouped: measured on MI355X
+// 7-10 % faster at M = 512 and 8192 on the 14336 x 4096 and 4096 x 14336
+// weights and 5 % on a 128-expert bank (1536 x 2048 and 2048 x 768 experts,
+// ~512 rows each). Split launches (small M) keep the LDS-weight kernels.
+// STM_FWD_RW_WM = 2 (eight waves, 128 x 64 wave tiles, the dequantization done
+// twice) measured 14 % slower.
 #ifndef STM_FWD_RW
 #define STM_FWD_RW 1
 #endif
@@ -1187,7 +1188,7 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
-    const bool rw = STM_FWD_RW && g.splits == 1 && g.num_groups == 1 && !g.offsets && rw_offsets_fit(g);
+    const bool rw = STM_FWD_RW && g.splits == 1 && rw_offsets_fit(g);
     const int rc = p.big ? (rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
                                        : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream))
                          : launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
