@@ -75,6 +75,7 @@ __device__ __forceinline__ int swz_key(int row) { return STM_SWZ ? ((row >> 1) &
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
 
 typedef __attribute__((address_space(3))) uint4 lds_uint4;
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t lds_offset(const uint4* p) {
     return (uint32_t)(size_t)((const lds_uint4*)(p));
@@ -235,7 +236,8 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[FA][FB]) {
 }
 
 // Rank-R term: acc[i][j] += Wside[rows] . Xside[cols]^T, both row-major with R contiguous.
-template <typename Tr, int FA, int FB>
+// Accumulator row r of fragment i is weight-side row wrow_base + 32 i + (r ^ CX).
+template <typename Tr, int FA, int FB, int CX = 0>
 __device__ __forceinline__ void lora_term(f32x16_t (&acc)[FA][FB], const uint16_t* __restrict__ wside,
                                           int64_t wrow_base, int64_t wrows, const uint16_t* __restrict__ xside,
                                           int64_t xrow_base, int64_t xrows, int R, int lane) {
@@ -243,7 +245,7 @@ __device__ __forceinline__ void lora_term(f32x16_t (&acc)[FA][FB], const uint16_
         uint4 a[FA], b[FB];
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
-            int64_t row = wrow_base + i * 32 + (lane & 31);
+            int64_t row = wrow_base + i * 32 + ((lane & 31) ^ CX);
             row = row < wrows ? row : wrows - 1;
             a[i] = *reinterpret_cast<const uint4*>(wside + row * R + r0 + 8 * (lane >> 5));
         }
@@ -671,10 +673,12 @@ __device__ __forceinline__ void mma_sub(f32x16_t (&acc)[2][FB], const uint4 (&w)
     }
 }
 
-// store_tile for k_gemm_fwd_rw: 32-bit element offsets from the tile's base
-// (the output has fewer than 2^31 elements), one row offset per fragment row
-// and compile-time column offsets, so few address registers are live.
-template <typename Tr, int FA, int FB>
+// store_tile for the register-weight kernels: 32-bit element offsets from the
+// tile's base (the output has fewer than 2^31 elements), one row offset per
+// fragment row and compile-time column offsets, so few address registers are
+// live. Accumulator row r holds output column r ^ CX (CX = 1: column pairs
+// swapped, as the input-gradient kernel's transposed weight reads deliver them).
+template <typename Tr, int FA, int FB, int CX = 0>
 __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
                                               int ocol_base, int ocols, int orow_base, int orows,
                                               const uint16_t* __restrict__ bias, int lane) {
@@ -686,7 +690,7 @@ __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uin
         for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int col = c0 + i * 32 + 8 * q + e;
+                const int col = c0 + i * 32 + 8 * q + (e ^ CX);
                 bv[i][q][e] = (bias && col < ocols) ? Tr::to_f32(bias[col]) : 0.0f;
             }
     const bool full = ocol_base + FA * 32 <= ocols;
@@ -707,13 +711,13 @@ __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uin
                 const int dc = i * 32 + 8 * q;
                 if (full) {
                     uint2 pk;
-                    pk.x = Tr::pack2(v[0], v[1]);
-                    pk.y = Tr::pack2(v[2], v[3]);
+                    pk.x = CX ? Tr::pack2(v[1], v[0]) : Tr::pack2(v[0], v[1]);
+                    pk.y = CX ? Tr::pack2(v[3], v[2]) : Tr::pack2(v[2], v[3]);
                     *reinterpret_cast<uint2*>(dst + dc) = pk;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (c0 + dc + e < ocols) dst[dc + e] = Tr::from_f32(v[e]);
+                        if (c0 + dc + (e ^ CX) < ocols) dst[dc + (e ^ CX)] = Tr::from_f32(v[e]);
                 }
             }
         }
@@ -980,6 +984,261 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     }
 }
 
+// -------------------------------------------- input gradient, register weights
+// dX tile BM x 256 (rows m x output columns k) with four waves; wave w owns the
+// 64 output columns [k0 + 64 w, k0 + 64 w + 64) over all BM rows, so, as in
+// k_gemm_fwd_rw, each wave dequantizes its own weight fragments into MFMA
+// operand registers. The MFMA's weight-side operand needs 8 consecutive
+// reduction indices n of one column k per lane -- a column of the row-major
+// packed weight. The packed tile (64 rows x 256 columns = 8 KB per step) is
+// copied into LDS and read back with ds_read_b64_tr_b4: within a 16-lane group,
+// lane i points at 16 packed columns of row i, and lane c receives nibble c of
+// the 16 rows, row r in nibble r -- 16 consecutive n of one column. Nibble c is
+// the low nibble of byte c / 2 for even c, and packed NF4 keeps the even column
+// in the high nibble, so lane c holds column c ^ 1: the accumulators' rows are
+// output columns in swapped pairs, undone by the store (and the LoRA term reads
+// its weight-side rows in the same order).
+//
+// Reduction order in a 64-deep step: lane half h at MFMA sub-step j takes rows
+// N(j, h) = 16 (2 (j / 2) + h) + 8 (j % 2) + (0..7); the activation (dY)
+// operand of lane (m, h) is LDS chunk N(j, h) / 8 of row m. Transposed read T
+// of fragment i (lanes of half h: rows 16 (2 T + h) + 0..15) covers sub-steps
+// 2 T (nibbles 0..7) and 2 T + 1 (nibbles 8..15). The absmax of a weight row
+// differs per n, so the step's absmax values [4 column blocks][64 rows] are
+// staged in LDS (1 KB) and each sub-step reads its 8 per half as two broadcast
+// 16-byte reads.
+//
+// Step s: copy dY(s + 1) and the packed tile of step s + 2 into LDS and load the
+// absmax of step s + 2; sub-steps 0..2 compute while step s + 1's fragments are
+// dequantized (transposed reads of its tile were done one step earlier); wait
+// for the copies, store the absmax, barrier; sub-step 3, during which step
+// s + 2's tile (published by that barrier) is read transposed. Launched for
+// unsplit problems.
+template <typename Tr>
+struct RwWeightsT {
+    struct Raw {
+        uint2 t[2][2];  // [fragment][transposed read T]
+    };
+    uint32_t lut_base, copy_off;
+
+    // transposed reads of one packed tile (buffer at LDS byte address tile)
+    __device__ __forceinline__ static void read(uint32_t tile, const uint32_t (&addr)[2][2], Raw& r) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+                const v2i32_t v = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+                    (__attribute__((address_space(3))) v2i32_t*)(size_t)(tile + addr[i][T]));
+                r.t[i][T] = make_uint2((uint32_t)v.x, (uint32_t)v.y);
+            }
+    }
+    // table reads of sub-step j (both fragments) and the sub-step's 8 absmax values
+    __device__ __forceinline__ void issue(const Raw& r, int j, f32x2_t (&p)[2][4], uint32_t absrow,
+                                          f32x4_t (&a)[2]) const {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t x = (j & 1) ? r.t[i][j >> 1].y : r.t[i][j >> 1].x;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t addr = __builtin_amdgcn_perm(copy_off, x, 0x0C0C0004u | ((uint32_t)b << 8));
+                p[i][b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)(lut_base + addr);
+            }
+        }
+        a[0] = *(const __attribute__((address_space(3))) f32x4_t*)(size_t)absrow;
+        a[1] = *(const __attribute__((address_space(3))) f32x4_t*)(size_t)(absrow + 16);
+    }
+    // byte b of a transposed word holds rows 2 b (low nibble) and 2 b + 1
+    __device__ __forceinline__ static void finish(const f32x2_t (&p)[2][4], const f32x4_t (&a)[2],
+                                                  uint4 (&out)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            out[i].x = Tr::pack2(opaque(p[i][0].y * a[0].x), opaque(p[i][0].x * a[0].y));
+            out[i].y = Tr::pack2(opaque(p[i][1].y * a[0].z), opaque(p[i][1].x * a[0].w));
+            out[i].z = Tr::pack2(opaque(p[i][2].y * a[1].x), opaque(p[i][2].x * a[1].y));
+            out[i].w = Tr::pack2(opaque(p[i][3].y * a[1].z), opaque(p[i][3].x * a[1].w));
+        }
+    }
+};
+
+template <typename Tr, int BM>
+__global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
+    constexpr int BN = 256, NT = 256, FB = BM / 32;
+    const int tid = threadIdx.x, lane0 = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    __shared__ float2 lut_all[256 * RW_LUT_COPIES];
+    __shared__ uint4 sA0[BM * 8], sA1[BM * 8];  // dY tiles [m][64 n]
+    __shared__ uint4 sW0[64 * 8], sW1[64 * 8];  // packed weight tiles [64 n][256 k / 2]
+    __shared__ float sS[3][4 * 64];             // absmax [column block][64 n], step s in sS[s % 3]
+
+    fill_lut_rw<NT>(lut_all, tid);
+
+    const int64_t K = g.K, N = g.N;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
+    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1); items (tile, expert)
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
+    const Group grp = group_of(g, (int)(w / tiles));
+    int64_t tm, tk;
+    tile_coords(w % tiles, ntm, ntk, tm, tk);
+    const int64_t m0 = tm * BM, k0 = tk * BN;
+    if (m0 >= grp.rows) continue;
+
+    const int KT = (int)(N / BK);
+    const int lane = opaque_lane(lane0);
+    const int bshift = 31 - __builtin_clz(g.blocksize);
+    const int64_t col_base = k0 + wave * 64;
+
+    // dY tile copies (as the forward's activation copies, leading dimension N)
+    ActStageS<BM, 4> as;
+    as.init(reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N, N, m0, grp.rows, sA0, sA1, wave, lane);
+
+    // packed-tile copies: slot S = 64 (4 i + wave) + lane of 512 16-byte slots,
+    // row r = S / 8, LDS chunk S % 8 holds packed chunk (S % 8) ^ key(r) of row r
+    // (columns past K re-read the row's last chunk; they feed unstored outputs)
+    uint32_t woff[2], wlds[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int S0 = 64 * (4 * i + wave);
+        const int r = (S0 + lane) >> 3, cs = lane & 7;
+        int64_t cb = k0 / 2 + 16 * (cs ^ swz_key(r));
+        cb = cb + 16 <= K / 2 ? cb : K / 2 - 16;
+        woff[i] = (uint32_t)(r * (K / 2) + cb);
+        wlds[i] = (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(sW0 + S0));
+    }
+    const uint32_t wstride = (uint32_t)(lds_offset(sW1) - lds_offset(sW0));
+    // absmax staging: lane = row n, wave = 64-column block of the tile
+    int64_t kcol = k0 + 64 * wave;
+    kcol = kcol < K ? kcol : K - 64;
+    const uint32_t aoff = (uint32_t)(lane * (K >> bshift) + (kcol >> bshift));
+    const uint32_t sS0 = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)&sS[0][0]);
+
+    // transposed-read addresses of fragment i, read T (relative to a tile buffer)
+    const int h = lane >> 5, cbk = (lane >> 4) & 1, rr = lane & 15;
+    uint32_t traddr[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const int r = 16 * (2 * T + h) + rr;
+            const int c = 2 * wave + i;
+            traddr[i][T] = (uint32_t)(16 * (r * 8 + (c ^ swz_key(r))) + 8 * cbk);
+        }
+    const uint32_t tile0 = lds_offset(sW0), tile1 = lds_offset(sW1);
+
+    RwWeightsT<Tr> ws;
+    ws.lut_base = (uint32_t)(size_t)((const __attribute__((address_space(3))) float2*)lut_all);
+    ws.copy_off = 8u * (uint32_t)(lane & 31);
+    // absmax row address of sub-step j, half h, in buffer b
+    auto absrow = [&](int b, int j) {
+        return sS0 + 4u * (uint32_t)(256 * b + 64 * wave + 16 * (2 * (j >> 1) + h) + 8 * (j & 1));
+    };
+
+    const uint8_t* pk = grp.packed;
+    const float* am = grp.absmax;
+    auto copy_w = [&](int s, int buf) {  // packed tile of step s -> sW[buf]
+        const uint8_t* base = pk + (int64_t)s * BK * (K / 2);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma16_s(base, woff[i], wlds[i] + (uint32_t)buf * wstride);
+    };
+    auto load_abs = [&](int s) { return am[(int64_t)s * BK * (K >> bshift) + aoff]; };
+    auto store_abs = [&](int buf, float v) {
+        *(__attribute__((address_space(3))) float*)(size_t)(sS0 + 4u * (uint32_t)(256 * buf + 64 * wave + lane)) = v;
+    };
+
+    f32x16_t acc[2][FB];
+    zero_acc(acc);
+    typename RwWeightsT<Tr>::Raw raw0, raw1;
+    uint4 B[4][2];
+    uint4 x[FB];
+    f32x2_t pa[2][4], pb[2][4];
+    f32x4_t aa[2], ab[2];
+    const int xh = lane >> 5;
+    auto xch = [&](int j) { return 4 * (j >> 1) + 2 * xh + (j & 1); };
+
+    // prologue: dY(0), packed tiles of steps 0 and 1, absmax of steps 0 and 1;
+    // fragments of sub-steps 0..2 of step 0, table reads of its sub-step 3
+    {
+        const float a0 = load_abs(0), a1 = load_abs(KT > 1 ? 1 : 0);
+        as.issue(0, 0);
+        copy_w(0, 0);
+        copy_w(KT > 1 ? 1 : 0, 1);
+        wait_vmem();
+        store_abs(0, a0);
+        store_abs(1, a1);  // absmax of step s in buffer s % 3
+    }
+    __syncthreads();  // level table, dY(0), tiles 0 and 1, absmax 0 and 1 ready
+    RwWeightsT<Tr>::read(tile0, traddr, raw0);
+    RwWeightsT<Tr>::read(tile1, traddr, raw1);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        ws.issue(raw0, j, pa, absrow(0, j), aa);
+        RwWeightsT<Tr>::finish(pa, aa, B[j]);
+    }
+    ws.issue(raw0, 3, pa, absrow(0, 3), aa);
+    // activation fragments of sub-step 0
+#pragma unroll
+    for (int f = 0; f < FB; ++f) x[f] = sA0[swz(f * 32 + (lane & 31), xch(0))];
+    __syncthreads();  // every wave has read tile 0 before step 0 copies into its buffer
+
+    auto sub = [&](const uint4 (&wf)[2], const uint4* sx, int jn, const typename RwWeightsT<Tr>::Raw& r_next,
+                   int j_next, uint32_t arow_next, f32x2_t (&p_next)[2][4], f32x4_t (&a_next)[2],
+                   const f32x2_t (&p_cur)[2][4], const f32x4_t (&a_cur)[2], uint4 (&bout)[2]) {
+        ws.issue(r_next, j_next, p_next, arow_next, a_next);
+        const int ch = xch(jn);
+#pragma unroll
+        for (int f = 0; f < FB; ++f) {
+            acc[0][f] = mfma<Tr>(wf[0], x[f], acc[0][f]);
+            acc[1][f] = mfma<Tr>(wf[1], x[f], acc[1][f]);
+            x[f] = sx[swz(f * 32 + (lane & 31), ch)];
+        }
+        RwWeightsT<Tr>::finish(p_cur, a_cur, bout);
+#pragma unroll
+        for (int k = 0; k < 2 * FB; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        sched_fence();
+    };
+
+    // step s: rawc = transposed tile of step s (its sub-step 3 not yet made),
+    // rawn = step s + 1; dY(s) in sAc; tiles alternate (step s in buffer cur),
+    // absmax buffers rotate over three (step s + 1 in a1, step s + 2 into a2buf,
+    // whose last reader, step s - 2's sub-step 3, is a barrier behind)
+    auto step = [&](int s, const uint4* sAc, const uint4* sAn, int cur, typename RwWeightsT<Tr>::Raw& rawc,
+                    const typename RwWeightsT<Tr>::Raw& rawn) {
+        const int s1 = s + 1 < KT ? s + 1 : KT - 1;
+        const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+        const int a1 = (s + 1) % 3, a2buf = (s + 2) % 3;
+        const float a2 = load_abs(s2);
+        as.issue((int64_t)s1 * BK, cur ^ 1);
+        copy_w(s2, cur);  // the tile of step s was read transposed one barrier ago
+        sub(B[0], sAc, 1, rawn, 0, absrow(a1, 0), pb, ab, pa, aa, B[3]);
+        sub(B[1], sAc, 2, rawn, 1, absrow(a1, 1), pa, aa, pb, ab, B[0]);
+        sub(B[2], sAc, 3, rawn, 2, absrow(a1, 2), pb, ab, pa, aa, B[1]);
+        wait_vmem();
+        store_abs(a2buf, a2);
+        __syncthreads();  // dY(s + 1), tile and absmax of step s + 2 ready; sAc free
+        RwWeightsT<Tr>::read(cur ? tile1 : tile0, traddr, rawc);  // step s + 2's tile into the freed registers
+        sub(B[3], sAn, 0, rawn, 3, absrow(a1, 3), pa, aa, pb, ab, B[2]);
+    };
+    int s = 0;
+    for (; s + 1 < KT; s += 2) {
+        step(s, sA0, sA1, 0, raw0, raw1);
+        step(s + 1, sA1, sA0, 1, raw1, raw0);
+    }
+    if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
+
+    const int lane_e = opaque_lane(lane);
+    if (g.lora_rank > 0)
+        lora_term<Tr, 2, FB, 1>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
+                                reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0, grp.rows,
+                                g.lora_rank, lane_e);
+    store_tile_rw<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
+                                (int)K, (int)m0, (int)grp.rows, nullptr, lane_e);
+    __syncthreads();
+    }
+}
+
 // Sum of the split partials [splits][rows][cols] (+ bias), one rounding; four
 // columns per lane (cols % 4 == 0).
 template <typename Tr>
@@ -1089,6 +1348,16 @@ int launch_bwd_cfg(const GemmArgs& g, int dtype, hipStream_t stream) {
 #define STM_FWD_RW 1
 #endif
 
+#ifndef STM_BWD_RW
+#define STM_BWD_RW 1
+#endif
+
+// k_gemm_bwd_rw: 32-bit offsets for dY [M, N], the packed weight, absmax and dX [M, K].
+bool rw_offsets_fit_bwd(const GemmArgs& g) {
+    const int64_t lim = (int64_t)1 << 32;
+    return g.M * g.N * 2 < lim && g.N * g.K / 2 < lim && g.N * g.K / g.blocksize < lim && g.M * g.K < lim / 2;
+}
+
 // k_gemm_fwd_rw addresses activations, packed weights and absmax of one group
 // with 32-bit offsets from uniform bases.
 bool rw_offsets_fit(const GemmArgs& g) {
@@ -1099,6 +1368,20 @@ bool rw_offsets_fit(const GemmArgs& g) {
 #ifndef STM_FWD_RW_WM
 #define STM_FWD_RW_WM 1
 #endif
+
+template <int BM>
+int launch_bwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
+    const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.K + 255) / 256);
+    if (tiles == 0) return STM_OK;
+    const int64_t work = tiles * g.num_groups;
+    if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
+    dim3 grid = work_grid(work), block(256);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemm_bwd_rw<BF16, BM>), grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL((k_gemm_bwd_rw<F16, BM>), grid, block, 0, stream, g);
+    return check_launch("gemm_bwd_dx");
+}
 
 template <int BM, int WM>
 int launch_fwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
@@ -1125,10 +1408,11 @@ namespace {
 //   waves(tiles * splits) * (steps_per_split * t_step + t_wave) + reduce,
 // t_step = time of one 64-deep step of one wave of tiles, measured at
 // M = 2048..8192 on the 14336 x 4096 and 4096 x 14336 weights (forward: 2.0 us
-// big tile, 0.8 us 128 x 128; input gradient: 2.4 us, 1.35 us), t_wave = 8 us
-// of per-tile prologue and epilogue, reduce = the fp32 partials written and
-// read once at 5 TB/s plus 4 us. Splits: at most 16, at least 8 steps each;
-// grouped launches never split.
+// big tile unsplit (register-weight kernel), 2.2 us split, 0.8 us 128 x 128;
+// input gradient: 1.85 us unsplit, 2.45 us split, 1.35 us), t_wave = 8 us of
+// per-tile prologue and epilogue, reduce = the fp32 partials written and read
+// once at 5 TB/s plus 4 us. Splits: at most 16, at least 8 steps each; grouped
+// launches never split.
 constexpr int kCUs = 256;
 
 struct Plan {
@@ -1150,16 +1434,17 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t big_tiles = ((M + bm - 1) / bm) * ((cols + bn - 1) / bn) * num_groups;
     const int64_t small_tiles = ((M + 127) / 128) * ((cols + 127) / 128) * num_groups;
     const int64_t steps = red / BK;
-    const double t_big = backward ? 2.4 : 2.0, t_small = backward ? 1.35 : 0.8;
+    // unsplit big tiles run the register-weight kernels
+    const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2, t_small = backward ? 1.35 : 0.8;
     int max_sp = 1;
     if (num_groups == 1) {
         const int64_t by_steps = steps / 8;
         max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
     }
     Plan best{true, big_tiles, 1};
-    double best_t = plan_cost(big_tiles, steps, 1, t_big, M, cols);
+    double best_t = plan_cost(big_tiles, steps, 1, t_big_rw, M, cols);
     for (int sp = 1; sp <= max_sp; ++sp) {
-        const double tb = plan_cost(big_tiles, steps, sp, t_big, M, cols);
+        const double tb = plan_cost(big_tiles, steps, sp, sp == 1 ? t_big_rw : t_big, M, cols);
         if (tb < best_t) {
             best_t = tb;
             best = Plan{true, big_tiles, sp};
@@ -1200,7 +1485,9 @@ int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.K, g.N, true, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
-    const int rc = p.big ? launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream)
+    const bool rw = STM_BWD_RW && g.splits == 1 && rw_offsets_fit_bwd(g);
+    const int rc = p.big ? (rw ? launch_bwd_rw<256>(g, dtype, stream)
+                                : launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream))
                          : launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.K, nullptr, dtype, stream);
