@@ -240,7 +240,7 @@ def run_lora_step(args):
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd_rw"),
                      "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
-        "bwd_dx": {"kernel": "k_gemm_bwd<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
+        "bwd_dx": {"kernel": "k_gemm_bwd_rw<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
         "dequant": {"kernel": "k_dequantize<BF16>", "value": round(deq_gbs, 1), "unit": "GB/s",
                     "frac": round(deq_gbs / HBM_PEAK_GBS, 4), "peak": HBM_PEAK_GBS,

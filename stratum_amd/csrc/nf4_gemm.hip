@@ -30,6 +30,8 @@
 // MFMA layout (v_mfma_f32_32x32x16): lane l supplies A[l % 32][k-group l / 32]
 // and B[k-group l / 32][l % 32] (8 halfs each; any k order common to A and B
 // gives the same product); result v of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "nf4_kernels.h"
@@ -1429,6 +1431,16 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
     return t;
 }
 
+// STRATUM_NF4_GEMM_TILE = "big" or "small" restricts the choice to one tile
+// shape (tests use it to reach each kernel); unset or anything else: cost model.
+int tile_override() {
+    const char* v = getenv("STRATUM_NF4_GEMM_TILE");
+    if (!v) return 0;
+    if (strcmp(v, "big") == 0) return 1;
+    if (strcmp(v, "small") == 0) return 2;
+    return 0;
+}
+
 Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t bm = backward ? STM_BWD_BM : STM_FWD_BM, bn = backward ? STM_BWD_BN : STM_FWD_BN;
     const int64_t big_tiles = ((M + bm - 1) / bm) * ((cols + bn - 1) / bn) * num_groups;
@@ -1441,16 +1453,17 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
         const int64_t by_steps = steps / 8;
         max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
     }
-    Plan best{true, big_tiles, 1};
-    double best_t = plan_cost(big_tiles, steps, 1, t_big_rw, M, cols);
+    const int only = tile_override();
+    Plan best{only != 2, only != 2 ? big_tiles : small_tiles, 1};
+    double best_t = 1e300;
     for (int sp = 1; sp <= max_sp; ++sp) {
         const double tb = plan_cost(big_tiles, steps, sp, sp == 1 ? t_big_rw : t_big, M, cols);
-        if (tb < best_t) {
+        if (only != 2 && tb < best_t) {
             best_t = tb;
             best = Plan{true, big_tiles, sp};
         }
         const double ts = plan_cost(small_tiles, steps, sp, t_small, M, cols);
-        if (ts < best_t) {
+        if (only != 1 && ts < best_t) {
             best_t = ts;
             best = Plan{false, small_tiles, sp};
         }

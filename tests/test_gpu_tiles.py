@@ -1,0 +1,174 @@
+"""Every GEMM kernel variant on the same ragged problems.
+
+The library picks, per call, the 256 x 256 tile (register-weight kernels when
+unsplit, LDS-weight kernels when the reduction is split) or the 128 x 128 tile,
+split or not. STRATUM_NF4_GEMM_TILE pins the tile shape and a call through the
+C ABI without a workspace pins "unsplit", so each kernel is reached on shapes
+whose rows, output columns and reduction are not multiples of the tile:
+results within the fp32-reference tolerance (1e-2 bf16, 5e-3 fp16) and, for
+the same problem, within rounding of each other.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle as C
+from oracle import nf4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-3}
+TAG = {torch.float16: O.DT_F16, torch.bfloat16: O.DT_BF16}
+
+
+def seeded(shape, seed, std, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+
+def rel(a, b):
+    a, b = a.float(), b.float()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def nf4(shape, seed, bs, dtype):
+    """(packed, absmax) of a seeded fp16 weight and its oracle dequantization in dtype (fp32)."""
+    w = seeded(shape, seed, 0.02, torch.float16)
+    bits = w.contiguous().view(torch.int16).numpy().view(np.uint16)
+    rp, ra = C.quantize(bits, O.DT_F16, bs, "argmin")
+    n = int(np.prod(shape))
+    deq = C.dequantize(rp, ra, n, bs, TAG[dtype]).view(np.int16).reshape(shape)
+    return torch.from_numpy(rp), torch.from_numpy(ra), torch.from_numpy(deq).view(dtype).float()
+
+
+def ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def fwd_abi(L, stream, x, packed, absmax, bias, t, lb, rank, N, K, bs, workspace=None):
+    from stratum_amd.functional import _gemm_dtype
+    M = x.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    nbytes = workspace.numel() * 4 if workspace is not None else 0
+    rc = L.stm_nf4_gemm_fwd(x.data_ptr(), packed.data_ptr(), absmax.data_ptr(), ptr(bias), ptr(t), ptr(lb), rank,
+                            y.data_ptr(), M, N, K, bs, _gemm_dtype(x), ptr(workspace), nbytes, stream)
+    assert rc == 0, L.stm_last_error()
+    return y
+
+
+def bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, workspace=None):
+    from stratum_amd.functional import _gemm_dtype
+    M = dy.shape[0]
+    dx = torch.empty((M, K), dtype=dy.dtype, device=dy.device)
+    nbytes = workspace.numel() * 4 if workspace is not None else 0
+    rc = L.stm_nf4_gemm_bwd_dx(dy.data_ptr(), packed.data_ptr(), absmax.data_ptr(), ptr(u), ptr(at), rank,
+                               dx.data_ptr(), M, N, K, bs, _gemm_dtype(dy), ptr(workspace), nbytes, stream)
+    assert rc == 0, L.stm_last_error()
+    return dx
+
+
+def variants(L, M, N, K, backward, monkeypatch, dev):
+    """(name, tile, workspace or None) for every kernel the problem can reach."""
+    out = []
+    for tile in ("big", "small"):
+        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+        out.append((tile + "-unsplit", tile, None))
+        nbytes = L.stm_nf4_gemm_workspace_bytes(M, N, K, int(backward))
+        if nbytes > 0:
+            out.append((tile + "-split", tile, torch.empty(nbytes // 4, dtype=torch.float32, device=dev)))
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,bs,bias,rank", [
+    (1, 64, 64, 64, False, 0),
+    (257, 520, 576, 64, True, 16),     # rows and columns past a tile edge
+    (300, 256, 512, 128, True, 32),    # blocksize 128
+    (64, 1000, 320, 64, False, 16),    # 1000 columns: last tile 232 wide
+    (33, 2048, 4096, 256, False, 0),   # small M: split reductions exist
+])
+def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
+    from stratum_amd import _lib
+    L = _lib.lib()
+    stream = _lib.stream_handle(cuda)
+    rp, ra, wq = nf4((N, K), M + N + K + bs, bs, dtype)
+    packed, absmax = rp.to(cuda), ra.to(cuda)
+    x = seeded((M, K), 1, 1.0, dtype).to(cuda)
+    b = seeded((N,), 2, 0.1, dtype).to(cuda) if bias else None
+    t = seeded((M, rank), 3, 0.5, dtype).to(cuda) if rank else None
+    lb = seeded((N, rank), 4, 0.01, dtype).to(cuda) if rank else None
+    ref = x.float() @ wq.to(cuda).t().contiguous()
+    if bias:
+        ref = ref + b.float()
+    if rank:
+        ref = ref + t.float() @ lb.float().t().contiguous()
+    results = {}
+    for name, tile, ws in variants(L, M, N, K, False, monkeypatch, cuda):
+        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+        y = fwd_abi(L, stream, x, packed, absmax, b, t, lb, rank, N, K, bs, ws)
+        assert rel(y, ref) <= TOL[dtype], name
+        results[name] = y
+    first = results["big-unsplit"]
+    for name, y in results.items():
+        assert rel(y, first) <= TOL[dtype] / 4, name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,bs,rank", [
+    (1, 64, 64, 64, 0),
+    (257, 192, 320, 64, 16),           # 320 output columns: second tile 64 wide
+    (300, 512, 384, 128, 32),          # blocksize 128, second tile 128 wide
+    (64, 128, 960, 64, 16),            # last tile 192 wide
+    (33, 4096, 2048, 64, 0),           # small M: split reductions exist
+])
+def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
+    from stratum_amd import _lib
+    L = _lib.lib()
+    stream = _lib.stream_handle(cuda)
+    rp, ra, wq = nf4((N, K), 3 * M + N + K + bs, bs, dtype)
+    packed, absmax = rp.to(cuda), ra.to(cuda)
+    dy = seeded((M, N), 5, 1.0, dtype).to(cuda)
+    u = seeded((M, rank), 6, 0.5, dtype).to(cuda) if rank else None
+    at = seeded((K, rank), 7, 0.01, dtype).to(cuda) if rank else None
+    ref = dy.float() @ wq.to(cuda)
+    if rank:
+        ref = ref + u.float() @ at.float().t().contiguous()
+    results = {}
+    for name, tile, ws in variants(L, M, N, K, True, monkeypatch, cuda):
+        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+        dx = bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, ws)
+        assert rel(dx, ref) <= TOL[dtype], name
+        results[name] = dx
+    first = results["big-unsplit"]
+    for name, dx in results.items():
+        assert rel(dx, first) <= TOL[dtype] / 4, name
+
+
+@pytest.mark.parametrize("tile", ["big", "small"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
+    """Expert banks with empty, tiny and tile-straddling experts; 320 columns in
+    the input gradient so its last tile is partly outside the matrix."""
+    from stratum_amd.functional import nf4_grouped_gemm
+    monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+    E, N, K = 6, 320, 320
+    w = seeded((E, N, K), 78, 0.02, torch.float16)
+    bits = w.reshape(-1, K).contiguous().view(torch.int16).numpy().view(np.uint16)
+    rp, ra = C.quantize(bits, O.DT_F16, 64, "argmin")
+    deq = C.dequantize(rp, ra, E * N * K, 64, TAG[dtype]).view(np.int16).reshape(E, N, K)
+    wq = torch.from_numpy(deq).view(dtype).float().to(cuda)
+    counts = [0, 3, 300, 1, 256, 70]
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    Mt = int(off[-1])
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    x = seeded((Mt, K), 8, 1.0, dtype).to(cuda)
+    dy = seeded((Mt, N), 9, 1.0, dtype).to(cuda)
+    y = nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), 64)
+    dx = nf4_grouped_gemm(dy, q, a, off.to(cuda), (N, K), 64, backward=True)
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], e
+        assert rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype], e
