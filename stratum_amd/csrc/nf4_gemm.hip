@@ -571,7 +571,9 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
 // configuration). Because no two waves along N share a weight column, each wave
 // dequantizes its weight fragments straight into MFMA operand registers: the
 // weight never goes through LDS, only the activation tile (shared by the waves)
-// and the level table do. Launched for unsplit problems (single-matrix and grouped).
+// and the level table do. Runs the unsplit 256 x 256 forwards (single-matrix and
+// grouped); it can also store a split's fp32 partial tile, but split forwards
+// measured faster on the LDS-weight kernel (see rw_split_ok).
 //
 // Reduction order inside a 64-deep step: lane half h = lane / 32 of a weight row
 // loads the 16 packed bytes of k in [32 h, 32 h + 32); MFMA sub-step j takes
@@ -615,6 +617,7 @@ struct RwWeights {
     const float* absmax;    // the group's absmax
     uint32_t woff[2];       // byte offset of this lane's 16-byte run of the first step, fragment i
     uint32_t aoff[2];       // absmax index of the start of weight row (fragment i)
+    int64_t kbase;          // first reduction index of the work item's step range
     int bshift;
     uint32_t lut_base;     // LDS byte address of the level table
     uint32_t copy_off;     // 8 * (lane % 32)
@@ -623,7 +626,7 @@ struct RwWeights {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             r.q[i] = *reinterpret_cast<const uint4*>(packed + (woff[i] + (uint32_t)(k0 / 2)));
-            r.a[i] = absmax[aoff[i] + (uint32_t)(k0 >> bshift)];
+            r.a[i] = absmax[aoff[i] + (uint32_t)((kbase + k0) >> bshift)];
         }
     }
     __device__ __forceinline__ static uint32_t word(const uint4& q, int j) {
@@ -726,6 +729,41 @@ __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uin
     }
 }
 
+// fp32 partial tile of one split for the register-weight kernels: the mapping of
+// store_tile_rw (CX as there), 16-byte runs, 32-bit offsets within the split's
+// [rows][ld] slice.
+template <int FA, int FB, int CX = 0>
+__device__ __forceinline__ void store_tile_f32_rw(const f32x16_t (&acc)[FA][FB], float* __restrict__ out, int ld,
+                                                  int ocol_base, int ocols, int orow_base, int orows, int lane) {
+    const int c0 = ocol_base + 4 * (lane >> 5);
+    const bool full = ocol_base + FA * 32 <= ocols;
+#pragma unroll
+    for (int j = 0; j < FB; ++j) {
+        const int orow = orow_base + j * 32 + (lane & 31);
+        if (orow >= orows) continue;
+        float* dst = out + (orow * ld + c0);
+#pragma unroll
+        for (int i = 0; i < FA; ++i) {
+            f32x16_t a = acc[i][j];
+            __asm__ volatile("" : "+v"(a));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int dc = i * 32 + 8 * q;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e ^ CX] = a[4 * q + e];
+                if (full) {
+                    *reinterpret_cast<float4*>(dst + dc) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c0 + dc + e < ocols) dst[dc + e] = v[e];
+                }
+            }
+        }
+    }
+}
+
 template <typename Tr, int BM, int WM>
 __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     constexpr int BN = 256, NT = 256 * WM, FB = BM / WM / 32;
@@ -739,16 +777,20 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
 
     const int64_t K = g.K, N = g.N;
     const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
-    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1); items (tile, expert)
-    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items as in k_gemm_fwd
-    const Group grp = group_of(g, (int)(w / tiles));
+    const int64_t work = tiles * g.num_groups * g.splits;
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items (tile, expert, split) as in k_gemm_fwd
+    const int64_t rest = w / tiles;
+    const int z = (int)(rest / g.num_groups);
+    const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tn;
     tile_coords(w % tiles, ntm, ntn, tm, tn);
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) continue;
 
-    const int KT = (int)(K / BK);
-    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K;
+    int s_begin, KT;
+    split_range((int)(K / BK), g.splits, z, s_begin, KT);
+    const int64_t kbase = (int64_t)s_begin * BK;
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K + kbase;
     const int lane = opaque_lane(lane0);
 
     RwWeights<Tr> ws;
@@ -758,11 +800,12 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     const int64_t col_base = n0 + wn * 64;
     ws.packed = grp.packed;
     ws.absmax = grp.absmax;
+    ws.kbase = kbase;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         int64_t n = col_base + i * 32 + (lane & 31);
         n = n < N ? n : N - 1;
-        ws.woff[i] = (uint32_t)(n * (K / 2) + 16 * (lane >> 5));
+        ws.woff[i] = (uint32_t)(n * (K / 2) + kbase / 2 + 16 * (lane >> 5));
         ws.aoff[i] = (uint32_t)(n * (K >> ws.bshift));
     }
     ActStageS<BM, 4 * WM> as;
@@ -837,12 +880,17 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
 
     const int lane_e = opaque_lane(lane);
-    if (g.lora_rank > 0)
+    if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, 2, FB>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
                              reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0 + xrow0, grp.rows,
                              g.lora_rank, lane_e);
-    store_tile_rw<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base, (int)N,
-                             (int)(m0 + xrow0), (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane_e);
+    if (g.splits > 1)
+        store_tile_f32_rw<2, FB>(acc, g.partial + (int64_t)z * g.M * N, (int)N, (int)col_base, (int)N,
+                                 (int)(m0 + xrow0), (int)grp.rows, lane_e);
+    else
+        store_tile_rw<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
+                                 (int)N, (int)(m0 + xrow0), (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias),
+                                 lane_e);
     __syncthreads();
     }
 }
@@ -1014,8 +1062,9 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
 // absmax of step s + 2; sub-steps 0..2 compute while step s + 1's fragments are
 // dequantized (transposed reads of its tile were done one step earlier); wait
 // for the copies, store the absmax, barrier; sub-step 3, during which step
-// s + 2's tile (published by that barrier) is read transposed. Launched for
-// unsplit problems.
+// s + 2's tile (published by that barrier) is read transposed. Runs the 256 x 256
+// input gradients, unsplit or split into ranges of >= 32 steps (a split's
+// work-group stores its fp32 partial tile).
 template <typename Tr>
 struct RwWeightsT {
     struct Raw {
@@ -1076,22 +1125,26 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 
     const int64_t K = g.K, N = g.N;
     const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
-    const int64_t work = tiles * g.num_groups;  // launched unsplit (splits == 1); items (tile, expert)
-    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
-    const Group grp = group_of(g, (int)(w / tiles));
+    const int64_t work = tiles * g.num_groups * g.splits;
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // items (tile, expert, split)
+    const int64_t rest = w / tiles;
+    const int z = (int)(rest / g.num_groups);
+    const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tk;
     tile_coords(w % tiles, ntm, ntk, tm, tk);
     const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) continue;
 
-    const int KT = (int)(N / BK);
+    int s_begin, KT;
+    split_range((int)(N / BK), g.splits, z, s_begin, KT);
     const int lane = opaque_lane(lane0);
     const int bshift = 31 - __builtin_clz(g.blocksize);
     const int64_t col_base = k0 + wave * 64;
 
     // dY tile copies (as the forward's activation copies, leading dimension N)
     ActStageS<BM, 4> as;
-    as.init(reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N, N, m0, grp.rows, sA0, sA1, wave, lane);
+    as.init(reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * N + (int64_t)s_begin * BK, N, m0, grp.rows, sA0, sA1,
+            wave, lane);
 
     // packed-tile copies: slot S = 64 (4 i + wave) + lane of 512 16-byte slots,
     // row r = S / 8, LDS chunk S % 8 holds packed chunk (S % 8) ^ key(r) of row r
@@ -1134,8 +1187,8 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
         return sS0 + 4u * (uint32_t)(256 * b + 64 * wave + 16 * (2 * (j >> 1) + h) + 8 * (j & 1));
     };
 
-    const uint8_t* pk = grp.packed;
-    const float* am = grp.absmax;
+    const uint8_t* pk = grp.packed + (int64_t)s_begin * BK * (K / 2);  // the split's first weight row
+    const float* am = grp.absmax + (int64_t)s_begin * BK * (K >> bshift);
     auto copy_w = [&](int s, int buf) {  // packed tile of step s -> sW[buf]
         const uint8_t* base = pk + (int64_t)s * BK * (K / 2);
 #pragma unroll
@@ -1231,12 +1284,16 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
     if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
 
     const int lane_e = opaque_lane(lane);
-    if (g.lora_rank > 0)
+    if (g.lora_rank > 0 && z == 0)
         lora_term<Tr, 2, FB, 1>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, K,
                                 reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0, grp.rows,
                                 g.lora_rank, lane_e);
-    store_tile_rw<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
-                                (int)K, (int)m0, (int)grp.rows, nullptr, lane_e);
+    if (g.splits > 1)
+        store_tile_f32_rw<2, FB, 1>(acc, g.partial + (int64_t)z * g.M * K, (int)K, (int)col_base, (int)K, (int)m0,
+                                    (int)grp.rows, lane_e);
+    else
+        store_tile_rw<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
+                                    (int)K, (int)m0, (int)grp.rows, nullptr, lane_e);
     __syncthreads();
     }
 }
@@ -1375,7 +1432,7 @@ template <int BM>
 int launch_bwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.K + 255) / 256);
     if (tiles == 0) return STM_OK;
-    const int64_t work = tiles * g.num_groups;
+    const int64_t work = tiles * g.num_groups * g.splits;
     if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_bwd_dx: grid too large");
     dim3 grid = work_grid(work), block(256);
     if (dtype == STM_BF16)
@@ -1389,7 +1446,7 @@ template <int BM, int WM>
 int launch_fwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + 255) / 256);
     if (tiles == 0) return STM_OK;
-    const int64_t work = tiles * g.num_groups;
+    const int64_t work = tiles * g.num_groups * g.splits;
     if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
     dim3 grid = work_grid(work), block(256 * WM);
     if (dtype == STM_BF16)
@@ -1410,8 +1467,8 @@ namespace {
 //   waves(tiles * splits) * (steps_per_split * t_step + t_wave) + reduce,
 // t_step = time of one 64-deep step of one wave of tiles, measured at
 // M = 2048..8192 on the 14336 x 4096 and 4096 x 14336 weights (forward: 2.0 us
-// big tile unsplit (register-weight kernel), 2.2 us split, 0.8 us 128 x 128;
-// input gradient: 1.85 us unsplit, 2.45 us split, 1.35 us), t_wave = 8 us of
+// big tile with the register-weight kernel, 2.2 us with the LDS-weight kernel,
+// 0.8 us 128 x 128; input gradient: 1.85 us, 2.45 us, 1.35 us), t_wave = 8 us of
 // per-tile prologue and epilogue, reduce = the fp32 partials written and read
 // once at 5 TB/s plus 4 us. Splits: at most 16, at least 8 steps each; grouped
 // launches never split.
@@ -1431,6 +1488,16 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
     return t;
 }
 
+// Whether a 256 x 256 launch of `splits` ranges over `steps` reduction steps runs
+// the register-weight kernel. Measured on MI355X: unsplit always wins; split, the
+// input gradient wins with at most 4 ranges of >= 32 steps (-14..-22 % at
+// M = 512..2048) and loses with more, shorter ranges (+11..+41 % at 7..16 ranges
+// of 14..32 steps); the split forward loses (+4..+20 %).
+bool rw_split_ok(bool backward, int splits, int64_t steps) {
+    if (splits <= 1) return true;
+    return backward && splits <= 4 && (steps + splits - 1) / splits >= 32;
+}
+
 // STRATUM_NF4_GEMM_TILE = "big" or "small" restricts the choice to one tile
 // shape (tests use it to reach each kernel); unset or anything else: cost model.
 int tile_override() {
@@ -1446,7 +1513,8 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t big_tiles = ((M + bm - 1) / bm) * ((cols + bn - 1) / bn) * num_groups;
     const int64_t small_tiles = ((M + 127) / 128) * ((cols + 127) / 128) * num_groups;
     const int64_t steps = red / BK;
-    // unsplit big tiles run the register-weight kernels
+    // big tiles run the register-weight kernels when unsplit, and for the input
+    // gradient also when split into ranges of >= 32 steps (rw_split_ok)
     const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2, t_small = backward ? 1.35 : 0.8;
     int max_sp = 1;
     if (num_groups == 1) {
@@ -1457,7 +1525,7 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     Plan best{only != 2, only != 2 ? big_tiles : small_tiles, 1};
     double best_t = 1e300;
     for (int sp = 1; sp <= max_sp; ++sp) {
-        const double tb = plan_cost(big_tiles, steps, sp, sp == 1 ? t_big_rw : t_big, M, cols);
+        const double tb = plan_cost(big_tiles, steps, sp, rw_split_ok(backward, sp, steps) ? t_big_rw : t_big, M, cols);
         if (only != 2 && tb < best_t) {
             best_t = tb;
             best = Plan{true, big_tiles, sp};
@@ -1486,7 +1554,7 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
-    const bool rw = STM_FWD_RW && g.splits == 1 && rw_offsets_fit(g);
+    const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
     const int rc = p.big ? (rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
                                        : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream))
                          : launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
@@ -1498,7 +1566,7 @@ int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.K, g.N, true, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
-    const bool rw = STM_BWD_RW && g.splits == 1 && rw_offsets_fit_bwd(g);
+    const bool rw = STM_BWD_RW && rw_split_ok(true, g.splits, g.N / BK) && rw_offsets_fit_bwd(g);
     const int rc = p.big ? (rw ? launch_bwd_rw<256>(g, dtype, stream)
                                 : launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream))
                          : launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
