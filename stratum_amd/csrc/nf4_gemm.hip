@@ -51,7 +51,7 @@
 #define STM_BWD_WN 2
 #endif
 #ifndef STM_GROUP_M
-#define STM_GROUP_M 8
+#define STM_GROUP_M 4
 #endif
 
 namespace stm {
@@ -138,7 +138,10 @@ __device__ __forceinline__ Group group_of(const GemmArgs& g, int e) {
 // Tile order: work-groups are dispatched round-robin over the 8 XCDs, so ids
 // i, i + 8, i + 16, ... share an L2. Give each XCD a contiguous run of tiles and
 // walk them GROUP_M activation tiles at a time so concurrently running tiles on
-// one XCD reuse the same activation rows and weight rows.
+// one XCD reuse the same activation rows and weight rows. With 32 CUs per XCD,
+// GROUP_M = 4 runs 4 activation x 8 weight tiles together; measured at
+// M = 8192 on W [14336, 4096] it fetches 735 MB per forward from beyond L2
+// (GROUP_M = 8: 1072 MB, 2: 820 MB) and is 1-4 % faster.
 __device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
     const int64_t T = ntm * ntn;
     const int64_t T8 = (T / 8) * 8;
