@@ -1477,8 +1477,12 @@ namespace {
 // launches never split.
 constexpr int kCUs = 256;
 
+// Tile kinds: kBig = 256 x 256 (register-weight or LDS-weight kernel), kSmall =
+// 128 x 128 (LDS-weight), kMid = 128 rows x 256 columns (register-weight, unsplit).
+enum TileKind { kBig = 0, kSmall = 1, kMid = 2 };
+
 struct Plan {
-    bool big;
+    int kind;
     int64_t tiles;
     int splits;
 };
@@ -1491,6 +1495,22 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
     return t;
 }
 
+// The 128 x 256 register-weight tile (kMid) as a cost-model choice for the input
+// gradient: measured at M = 512..4096 on the 14336 x 4096 and 4096 x 14336
+// weights it is 0-12 % faster than the choices without it there; for the
+// forward it measured -3..+5 %, so the forward uses it only when pinned
+// (STRATUM_NF4_GEMM_TILE=mid). Per-step times calibrated at M = 4096, N = 2048,
+// K = 1024..4096 (256 tiles): forward 1.28 us, input gradient 1.08 us.
+#ifndef STM_MID_TILE
+#define STM_MID_TILE 1
+#endif
+#ifndef STM_T_MID_FWD
+#define STM_T_MID_FWD 1.3
+#endif
+#ifndef STM_T_MID_BWD
+#define STM_T_MID_BWD 1.1
+#endif
+
 // Whether a 256 x 256 launch of `splits` ranges over `steps` reduction steps runs
 // the register-weight kernel. Measured on MI355X: unsplit always wins; split, the
 // input gradient wins with at most 4 ranges of >= 32 steps (-14..-22 % at
@@ -1501,42 +1521,52 @@ bool rw_split_ok(bool backward, int splits, int64_t steps) {
     return backward && splits <= 4 && (steps + splits - 1) / splits >= 32;
 }
 
-// STRATUM_NF4_GEMM_TILE = "big" or "small" restricts the choice to one tile
-// shape (tests use it to reach each kernel); unset or anything else: cost model.
+// STRATUM_NF4_GEMM_TILE = "big", "mid" or "small" restricts the choice to one
+// tile kind (tests use it to reach each kernel); unset or anything else: cost model.
 int tile_override() {
     const char* v = getenv("STRATUM_NF4_GEMM_TILE");
-    if (!v) return 0;
-    if (strcmp(v, "big") == 0) return 1;
-    if (strcmp(v, "small") == 0) return 2;
-    return 0;
+    if (!v) return -1;
+    if (strcmp(v, "big") == 0) return kBig;
+    if (strcmp(v, "small") == 0) return kSmall;
+    if (strcmp(v, "mid") == 0) return kMid;
+    return -1;
 }
 
 Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t bm = backward ? STM_BWD_BM : STM_FWD_BM, bn = backward ? STM_BWD_BN : STM_FWD_BN;
     const int64_t big_tiles = ((M + bm - 1) / bm) * ((cols + bn - 1) / bn) * num_groups;
     const int64_t small_tiles = ((M + 127) / 128) * ((cols + 127) / 128) * num_groups;
+    const int64_t mid_tiles = ((M + 127) / 128) * ((cols + 255) / 256) * num_groups;
     const int64_t steps = red / BK;
     // big tiles run the register-weight kernels when unsplit, and for the input
     // gradient also when split into ranges of >= 32 steps (rw_split_ok)
     const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2, t_small = backward ? 1.35 : 0.8;
+    const double t_mid = backward ? STM_T_MID_BWD : STM_T_MID_FWD;
     int max_sp = 1;
     if (num_groups == 1) {
         const int64_t by_steps = steps / 8;
         max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
     }
     const int only = tile_override();
-    Plan best{only != 2, only != 2 ? big_tiles : small_tiles, 1};
+    Plan best{only < 0 ? (int)kBig : only, only == kSmall ? small_tiles : only == kMid ? mid_tiles : big_tiles, 1};
     double best_t = 1e300;
     for (int sp = 1; sp <= max_sp; ++sp) {
         const double tb = plan_cost(big_tiles, steps, sp, rw_split_ok(backward, sp, steps) ? t_big_rw : t_big, M, cols);
-        if (only != 2 && tb < best_t) {
+        if ((only < 0 || only == kBig) && tb < best_t) {
             best_t = tb;
-            best = Plan{true, big_tiles, sp};
+            best = Plan{kBig, big_tiles, sp};
         }
         const double ts = plan_cost(small_tiles, steps, sp, t_small, M, cols);
-        if (only != 1 && ts < best_t) {
+        if ((only < 0 || only == kSmall) && ts < best_t) {
             best_t = ts;
-            best = Plan{false, small_tiles, sp};
+            best = Plan{kSmall, small_tiles, sp};
+        }
+        if (sp == 1 && (STM_MID_TILE || only == kMid) && (backward || only == kMid)) {
+            const double tm = plan_cost(mid_tiles, steps, 1, t_mid, M, cols);
+            if ((only < 0 || only == kMid) && tm < best_t) {
+                best_t = tm;
+                best = Plan{kMid, mid_tiles, 1};
+            }
         }
     }
     return best;
@@ -1558,9 +1588,14 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
-    const int rc = p.big ? (rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
-                                       : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream))
-                         : launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+    int rc;
+    if (p.kind == kMid && rw_offsets_fit(g))
+        rc = launch_fwd_rw<128, 1>(g, dtype, stream);
+    else if (p.kind == kBig || p.kind == kMid)
+        rc = rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
+                : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream);
+    else
+        rc = launch_fwd_cfg<128, 128, 2, 2>(g, dtype, stream);
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.N, g.bias, dtype, stream);
 }
@@ -1570,9 +1605,14 @@ int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     const Plan p = plan(g.M, g.K, g.N, true, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_BWD_RW && rw_split_ok(true, g.splits, g.N / BK) && rw_offsets_fit_bwd(g);
-    const int rc = p.big ? (rw ? launch_bwd_rw<256>(g, dtype, stream)
-                                : launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream))
-                         : launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
+    int rc;
+    if (p.kind == kMid && rw_offsets_fit_bwd(g))
+        rc = launch_bwd_rw<128>(g, dtype, stream);
+    else if (p.kind == kBig || p.kind == kMid)
+        rc = rw ? launch_bwd_rw<256>(g, dtype, stream)
+                : launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream);
+    else
+        rc = launch_bwd_cfg<128, 128, 2, 2>(g, dtype, stream);
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.K, nullptr, dtype, stream);
 }

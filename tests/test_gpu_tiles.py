@@ -1,10 +1,11 @@
 """Every GEMM kernel variant on the same ragged problems.
 
-The library picks, per call, the 256 x 256 tile (register-weight kernels when
-unsplit, LDS-weight kernels when the reduction is split) or the 128 x 128 tile,
-split or not. STRATUM_NF4_GEMM_TILE pins the tile shape and a call through the
-C ABI without a workspace pins "unsplit", so each kernel is reached on shapes
-whose rows, output columns and reduction are not multiples of the tile:
+The library picks, per call, the 256 x 256 tile (register-weight kernels, or
+LDS-weight kernels for some split reductions), the 128 x 256 register-weight
+tile (unsplit) or the 128 x 128 LDS-weight tile, split or not.
+STRATUM_NF4_GEMM_TILE pins the tile kind and a call through the C ABI without a
+workspace pins "unsplit", so each kernel is reached on shapes whose rows,
+output columns and reduction are not multiples of the tile:
 results within the fp32-reference tolerance (1e-2 bf16, 5e-3 fp16) and, for
 the same problem, within rounding of each other.
 """
@@ -71,7 +72,7 @@ def bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, workspace=None
 def variants(L, M, N, K, backward, monkeypatch, dev):
     """(name, tile, workspace or None) for every kernel the problem can reach."""
     out = []
-    for tile in ("big", "small"):
+    for tile in ("big", "mid", "small"):
         monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
         out.append((tile + "-unsplit", tile, None))
         nbytes = L.stm_nf4_gemm_workspace_bytes(M, N, K, int(backward))
@@ -145,7 +146,7 @@ def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank
         assert rel(dx, first) <= TOL[dtype] / 4, name
 
 
-@pytest.mark.parametrize("tile", ["big", "small"])
+@pytest.mark.parametrize("tile", ["big", "mid", "small"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
     """Expert banks with empty, tiny and tile-straddling experts; 320 columns in
