@@ -70,6 +70,16 @@ __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f
                                                       0, 0, 0);
 }
 
+template <typename Tr>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, const f32x4_t& c) {
+    if constexpr (Tr::tag == STM_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                      0, 0, 0);
+}
+
 #ifndef STM_SWZ
 #define STM_SWZ 1
 #endif
@@ -222,12 +232,34 @@ struct ActStageS {
 // random byte values collide on banks several times per read).
 constexpr int LUT_COPIES = 16;
 
+// Level i (0..15) of the codebook from immediates: no memory access.
+__device__ __forceinline__ float level_from_immediates(int i) {
+    float v = kLevelsDev[0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) v = i == k ? kLevelsDev[k] : v;
+    return v;
+}
+
+// Entries (level[b >> 4], level[b & 15]) at index copies * b + c, written by NT
+// threads: lane l holds level l % 16 and each entry gathers its two levels
+// across lanes, so filling costs no memory round trips (a load per entry
+// would put a dozen dependent round trips at the start of every block).
+template <int NT, int COPIES>
+__device__ __forceinline__ void fill_level_table(float2* lut, int tid) {
+    static_assert((256 * COPIES) % NT == 0, "every thread writes the same number of entries");
+    const int mine = __float_as_int(level_from_immediates(tid & 15));
+#pragma unroll
+    for (int i = 0; i < 256 * COPIES / NT; ++i) {
+        const int t = tid + NT * i, b = t / COPIES;
+        const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((b >> 4) << 2, mine));
+        const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((b & 15) << 2, mine));
+        lut[t] = make_float2(hi, lo);
+    }
+}
+
 template <int NT>
 __device__ __forceinline__ void fill_lut(float2* lut, int tid) {
-    for (int t = tid; t < 256 * LUT_COPIES; t += NT) {
-        const int b = t / LUT_COPIES;
-        lut[t] = make_float2(kLevelsDev[b >> 4], kLevelsDev[b & 15]);
-    }
+    fill_level_table<NT, LUT_COPIES>(lut, tid);
 }
 
 template <int FA, int FB>
@@ -604,10 +636,7 @@ constexpr int RW_LUT_COPIES = 32;
 
 template <int NT>
 __device__ __forceinline__ void fill_lut_rw(float2* lut, int tid) {
-    for (int t = tid; t < 256 * RW_LUT_COPIES; t += NT) {
-        const int b = t / RW_LUT_COPIES;
-        lut[t] = make_float2(kLevelsDev[b >> 4], kLevelsDev[b & 15]);
-    }
+    fill_level_table<NT, RW_LUT_COPIES>(lut, tid);
 }
 
 template <typename Tr>
@@ -1301,12 +1330,146 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
     }
 }
 
-// Sum of the split partials [splits][rows][cols] (+ bias), one rounding; four
-// columns per lane (cols % 4 == 0).
+// ------------------------------------------------------------ small-M forward
+// Y[M, N] = X[M, K] . W[N, K]^T for M <= 16 rows (decode-sized batches),
+// where streaming the weight, not the MFMA, is the bound. Each wave owns
+// 16 R weight rows (R tiles of v_mfma_f32_16x16x32, weight rows x activation
+// rows) over one reduction range; the weight-side operand is dequantized in
+// registers as in k_gemm_fwd_rw and the activation operand comes straight from
+// memory, shared by the R tiles. A 128-deep chunk: lane (r = lane % 16,
+// h = lane / 16) loads 16 packed bytes (k = 32 h + 0..31) of row r of each
+// tile and one absmax, and MFMA q (0..3) of the chunk takes k = 32 h + 8 q +
+// (0..7) from both operands, so every load instruction reads 64 contiguous
+// bytes of each of 16 rows. The bound is the L1 access rate: the operand
+// layout puts neighbouring lanes on different rows, so each lane's 16 bytes
+// cost an access of their own. K % 128 == 64 leaves the upper half of the last chunk empty: those
+// lanes read the row start with a zero scale and zero activations. Reduction
+// ranges (splits) write fp32 partials [split][m][n] that k_split_reduce sums
+// (with bias and the LoRA term); with one range the output (plus bias) is
+// stored directly.
+#ifndef STM_GEMV_U
+#define STM_GEMV_U 2
+#endif
+#ifndef STM_GEMV_WAVES
+#define STM_GEMV_WAVES 4
+#endif
+template <typename Tr, int R>
+__global__ __launch_bounds__(64 * STM_GEMV_WAVES) void k_gemv_fwd(GemmArgs g, int chunks_per_split) {
+    constexpr int U = STM_GEMV_U;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ float2 lut_all[256 * RW_LUT_COPIES];
+    fill_lut_rw<64 * STM_GEMV_WAVES>(lut_all, tid);
+    __syncthreads();
+
+    const int64_t K = g.K, N = g.N, M = g.M;
+    const int bshift = 31 - __builtin_clz(g.blocksize);
+    const int64_t n0 = ((int64_t)blockIdx.x * STM_GEMV_WAVES + wave) * (16 * R);
+    const int z = blockIdx.y;
+    const int nchunks = (int)((K + 127) / 128);
+    const int c_begin = z * chunks_per_split;
+    int c_end = c_begin + chunks_per_split;
+    c_end = c_end < nchunks ? c_end : nchunks;
+    const int r = lane & 15, h = lane >> 4;
+    const uint8_t* wrow[R];
+    const float* arow[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        int64_t n = n0 + 16 * t + r;
+        n = n < N ? n : N - 1;
+        wrow[t] = g.packed + n * (K / 2);
+        arow[t] = g.absmax + n * (K >> bshift);
+    }
+    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(g.a) + (r < M ? r : M - 1) * K;
+    const uint32_t lut_base = (uint32_t)(size_t)((const __attribute__((address_space(3))) float2*)lut_all);
+    const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
+
+    f32x4_t acc[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // U chunks per group: all loads of a group, then its dequantization and
+    // MFMAs; other waves of the CU hide the latency
+    for (int c0 = c_begin; c0 < c_end; c0 += U) {
+        uint4 q[U][R];
+        float a[U][R];
+        uint4 xv[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u;
+            const int k = 128 * c + 32 * h;
+            // chunks past the range and the empty half of a last chunk read
+            // the row start and contribute zeros
+            const bool ok = c < c_end && k < K;
+            const int64_t wo = ok ? k / 2 : 0, xo = ok ? k : 0;
+            const int ai = ok ? (k >> bshift) : 0;
+#pragma unroll
+            for (int t = 0; t < R; ++t) {
+                q[u][t] = *reinterpret_cast<const uint4*>(wrow[t] + wo);
+                const float av = arow[t][ai];
+                a[u][t] = ok ? av : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xrow + xo + 8 * j);
+                xv[u][j] = ok ? v : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int t = 0; t < R; ++t) {
+                    const uint32_t word = j == 0 ? q[u][t].x : j == 1 ? q[u][t].y : j == 2 ? q[u][t].z : q[u][t].w;
+                    f32x2_t p[4];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t addr =
+                            __builtin_amdgcn_perm(copy_off, word, 0x0C0C0004u | ((uint32_t)b << 8));
+                        p[b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)(lut_base + addr);
+                    }
+                    const float av = a[u][t];
+                    uint4 w;
+                    w.x = Tr::pack2(opaque(p[0].x * av), opaque(p[0].y * av));
+                    w.y = Tr::pack2(opaque(p[1].x * av), opaque(p[1].y * av));
+                    w.z = Tr::pack2(opaque(p[2].x * av), opaque(p[2].y * av));
+                    w.w = Tr::pack2(opaque(p[3].x * av), opaque(p[3].y * av));
+                    acc[t] = mfma16<Tr>(w, xv[u][j], acc[t]);
+                }
+            }
+        }
+    }
+
+    // C[4 h + i][r] of tile t: weight row n0 + 16 t + 4 h + i, activation row r
+    const uint16_t* bias = reinterpret_cast<const uint16_t*>(g.bias);
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const int64_t m = r;
+        const int64_t nc = n0 + 16 * t + 4 * h;
+        if (m >= M || nc >= N) continue;  // N % 8 == 0: all four columns valid
+        if (g.splits > 1) {
+            *reinterpret_cast<float4*>(g.partial + (int64_t)z * M * N + m * N + nc) =
+                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        } else {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = acc[t][i] + (bias ? Tr::to_f32(bias[nc + i]) : 0.0f);
+            uint2 pk;
+            pk.x = Tr::pack2(v[0], v[1]);
+            pk.y = Tr::pack2(v[2], v[3]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * N + nc) = pk;
+        }
+    }
+}
+
+// Sum of the split partials [splits][rows][cols] (+ bias) (+ T[row] . L[col]
+// over R ranks, when R > 0), one rounding; four columns per lane (cols % 4 == 0).
 template <typename Tr>
 __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ partial, int splits, int64_t rows,
                                                       int64_t cols, const uint16_t* __restrict__ bias,
-                                                      uint16_t* __restrict__ out) {
+                                                      const uint16_t* __restrict__ T, const uint16_t* __restrict__ L,
+                                                      int R, uint16_t* __restrict__ out) {
     const int64_t total = rows * (cols / 4), plane = rows * cols;
     for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < total; v += (int64_t)gridDim.x * blockDim.x) {
         const int64_t e = v * 4;
@@ -1317,6 +1480,22 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
             acc.y += p.y;
             acc.z += p.z;
             acc.w += p.w;
+        }
+        if (R > 0) {
+            const int64_t row = e / cols, c = e % cols;
+            const uint16_t* t = T + row * R;
+            float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
+            for (int k = 0; k < R; ++k) {
+                const float tk = Tr::to_f32(t[k]);
+                l0 += tk * Tr::to_f32(L[(c + 0) * R + k]);
+                l1 += tk * Tr::to_f32(L[(c + 1) * R + k]);
+                l2 += tk * Tr::to_f32(L[(c + 2) * R + k]);
+                l3 += tk * Tr::to_f32(L[(c + 3) * R + k]);
+            }
+            acc.x += l0;
+            acc.y += l1;
+            acc.z += l2;
+            acc.w += l3;
         }
         if (bias) {
             const int64_t c = e % cols;
@@ -1332,18 +1511,71 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
     }
 }
 
-int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int dtype, hipStream_t stream) {
+// lora: add the rank-R term here (the small-M forward leaves it to the reduce)
+int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int dtype, hipStream_t stream,
+                        bool lora = false) {
     const int64_t items = g.M * (cols / 4);
     if (items == 0) return STM_OK;
     const int64_t blocks = (items + 255) / 256;
     const unsigned grid = (unsigned)(blocks < 16384 ? blocks : 16384);
+    const int R = lora ? g.lora_rank : 0;
+    const uint16_t* T = R ? (const uint16_t*)g.lora_x : nullptr;
+    const uint16_t* L = R ? (const uint16_t*)g.lora_w : nullptr;
     if (dtype == STM_BF16)
         hipLaunchKernelGGL(k_split_reduce<BF16>, dim3(grid), dim3(256), 0, stream, g.partial, g.splits, g.M, cols,
-                           (const uint16_t*)bias, (uint16_t*)g.out);
+                           (const uint16_t*)bias, T, L, R, (uint16_t*)g.out);
     else
         hipLaunchKernelGGL(k_split_reduce<F16>, dim3(grid), dim3(256), 0, stream, g.partial, g.splits, g.M, cols,
-                           (const uint16_t*)bias, (uint16_t*)g.out);
+                           (const uint16_t*)bias, T, L, R, (uint16_t*)g.out);
     return check_launch("gemm split reduce");
+}
+
+#ifndef STM_GEMV_MAX_M
+#define STM_GEMV_MAX_M 16
+#endif
+
+#ifndef STM_GEMV_TARGET
+#define STM_GEMV_TARGET 2048
+#endif
+// Small-M forward: weight row tiles per wave (4 for wide weights, where fewer
+// activation loads per weight byte pay; 2 otherwise, for more waves).
+int gemv_tiles(int64_t N) { return N >= 8192 ? 4 : 2; }
+
+// Reduction ranges so that about STM_GEMV_TARGET waves stream weights
+// (N / (16 R) waves per range), at least 4 chunks of 128 per range.
+int gemv_splits(int64_t N, int64_t K) {
+    const int rows = 16 * gemv_tiles(N);
+    const int64_t waves = (N + rows - 1) / rows, chunks = (K + 127) / 128;
+    int64_t sp = (STM_GEMV_TARGET + waves - 1) / waves;
+    const int64_t max_sp = chunks / 4 > 1 ? chunks / 4 : 1;
+    sp = sp < max_sp ? sp : max_sp;
+    return (int)(sp < 1 ? 1 : sp);
+}
+
+bool use_gemv(int64_t M, int num_groups) { return num_groups == 1 && M > 0 && M <= STM_GEMV_MAX_M; }
+
+int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
+    const int nchunks = (int)((g.K + 127) / 128);
+    const int cps = (nchunks + g.splits - 1) / g.splits;
+    const int splits = cps ? (nchunks + cps - 1) / cps : 1;  // every range non-empty (K = 0: one empty range)
+    g.splits = splits;
+    const int R = gemv_tiles(g.N);
+    const int rows_per_block = 16 * R * STM_GEMV_WAVES;
+    dim3 grid((unsigned)((g.N + rows_per_block - 1) / rows_per_block), (unsigned)splits), block(64 * STM_GEMV_WAVES);
+    if (R == 4) {
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, 4>), grid, block, 0, stream, g, cps);
+        else
+            hipLaunchKernelGGL((k_gemv_fwd<F16, 4>), grid, block, 0, stream, g, cps);
+    } else {
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, 2>), grid, block, 0, stream, g, cps);
+        else
+            hipLaunchKernelGGL((k_gemv_fwd<F16, 2>), grid, block, 0, stream, g, cps);
+    }
+    int rc = check_launch("gemm_fwd (small M)");
+    if (rc != STM_OK || g.splits == 1) return rc;
+    return launch_split_reduce(g, g.N, g.bias, dtype, stream, true);
 }
 
 #ifndef STM_PERSISTENT
@@ -1579,12 +1811,28 @@ int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) 
 }
 
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
+    // small M: room for either kernel (a pinned tile kind skips the small-M one)
+    int64_t gemv_need = 0;
+    if (!backward && use_gemv(M, num_groups)) {
+        const int sp = gemv_splits(N, K);
+        gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
+    }
     const int sp = gemm_splits(M, N, K, backward, num_groups);
-    return sp > 1 ? (int64_t)sp * M * (backward ? K : N) * (int64_t)sizeof(float) : 0;
+    const int64_t need = sp > 1 ? (int64_t)sp * M * (backward ? K : N) * (int64_t)sizeof(float) : 0;
+    return need > gemv_need ? need : gemv_need;
 }
 
 int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
+    // small M: the weight-streaming kernel, when its partials have a workspace
+    // (or it needs none) and the LoRA term can go to the reduce
+    if (use_gemv(g.M, g.num_groups) && tile_override() < 0) {
+        const int sp = gemv_splits(g.N, g.K);
+        if (sp == 1 ? g.lora_rank == 0 : g.partial != nullptr) {
+            g.splits = sp;
+            return launch_gemv_fwd(g, dtype, stream);
+        }
+    }
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);

@@ -135,13 +135,18 @@ def test_gemm_workspace_sizing(L):
     # large problems fill the GPU with output tiles: no split, no workspace
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 1) == 0
-    # M = 16, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
-    # the input gradient's 16 big tiles (4096 output columns) split 16 ways
-    # over the 224 steps of its 14336-long reduction
-    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 2 * 16 * 14336 * 4
+    # M = 17, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
+    # M = 16: the input gradient's 16 big tiles (4096 output columns) split 16
+    # ways over the 224 steps of its 14336-long reduction
+    assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 2 * 17 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
-    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 8 * 1 * 4096 * 4
-    # a short reduction caps the split at 8 steps per split
+    # forward with M <= 16: the small-M kernel's ranges (about 2048 waves of 64
+    # weight rows for N >= 8192, else 32 rows; at least 4 chunks of 128 each):
+    # 224 waves x 8 ranges (32 chunks); 128 waves x 16 ranges
+    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 8 * 16 * 14336 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 16 * 1 * 4096 * 4
+    # a short reduction caps the split: 8 steps per tile-path range, 4 chunks
+    # per small-M range (both give 2 here)
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 256, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(0, 256, 4096, 0) == 0

@@ -2,10 +2,13 @@
 
 The library picks, per call, the 256 x 256 tile (register-weight kernels, or
 LDS-weight kernels for some split reductions), the 128 x 256 register-weight
-tile (unsplit) or the 128 x 128 LDS-weight tile, split or not.
-STRATUM_NF4_GEMM_TILE pins the tile kind and a call through the C ABI without a
-workspace pins "unsplit", so each kernel is reached on shapes whose rows,
-output columns and reduction are not multiples of the tile:
+tile (unsplit) or the 128 x 128 LDS-weight tile, split or not, and for a
+forward of at most 16 rows the weight-streaming small-M kernel (its reduction
+ranges summed by the split-reduce kernel, which adds bias and the LoRA term).
+STRATUM_NF4_GEMM_TILE pins the tile kind (and so skips the small-M kernel) and
+a call through the C ABI without a workspace pins "unsplit", so each kernel is
+reached on shapes whose rows, output columns and reduction are not multiples
+of the tile:
 results within the fp32-reference tolerance (1e-2 bf16, 5e-3 fp16) and, for
 the same problem, within rounding of each other.
 """
@@ -69,15 +72,24 @@ def bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, workspace=None
     return dx
 
 
-def variants(L, M, N, K, backward, monkeypatch, dev):
-    """(name, tile, workspace or None) for every kernel the problem can reach."""
-    out = []
-    for tile in ("big", "mid", "small"):
+def set_tile(monkeypatch, tile):
+    if tile is None:
+        monkeypatch.delenv("STRATUM_NF4_GEMM_TILE", raising=False)
+    else:
         monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
-        out.append((tile + "-unsplit", tile, None))
+
+
+def variants(L, M, N, K, backward, monkeypatch, dev):
+    """(name, tile, workspace or None) for every kernel the problem can reach;
+    tile None is the library's own choice (the small-M kernel where it applies)."""
+    out = []
+    for tile in (None, "big", "mid", "small"):
+        set_tile(monkeypatch, tile)
+        name = tile or "auto"
+        out.append((name + "-unsplit", tile, None))
         nbytes = L.stm_nf4_gemm_workspace_bytes(M, N, K, int(backward))
         if nbytes > 0:
-            out.append((tile + "-split", tile, torch.empty(nbytes // 4, dtype=torch.float32, device=dev)))
+            out.append((name + "-split", tile, torch.empty(nbytes // 4, dtype=torch.float32, device=dev)))
     return out
 
 
@@ -88,6 +100,12 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (300, 256, 512, 128, True, 32),    # blocksize 128
     (64, 1000, 320, 64, False, 16),    # 1000 columns: last tile 232 wide
     (33, 2048, 4096, 256, False, 0),   # small M: split reductions exist
+    (16, 520, 576, 64, True, 16),      # small-M kernel: 520 columns, K % 128 == 64 (half-empty last chunk)
+    (5, 4096, 1024, 128, True, 32),    # small-M kernel, blocksize 128, bias + LoRA in the reduce
+    (12, 264, 4160, 64, False, 16),    # small-M kernel: 33 chunks over uneven ranges
+    (15, 8, 64, 64, True, 0),          # one half chunk, eight columns, unsplit with bias
+    (3, 8192, 320, 64, True, 0),       # four row tiles per wave, unsplit, half-empty last chunk
+    (9, 8200, 1024, 256, True, 16),    # four row tiles per wave, split, last block partly outside
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
@@ -106,7 +124,7 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
         ref = ref + t.float() @ lb.float().t().contiguous()
     results = {}
     for name, tile, ws in variants(L, M, N, K, False, monkeypatch, cuda):
-        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+        set_tile(monkeypatch, tile)
         y = fwd_abi(L, stream, x, packed, absmax, b, t, lb, rank, N, K, bs, ws)
         assert rel(y, ref) <= TOL[dtype], name
         results[name] = y
@@ -137,7 +155,7 @@ def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank
         ref = ref + u.float() @ at.float().t().contiguous()
     results = {}
     for name, tile, ws in variants(L, M, N, K, True, monkeypatch, cuda):
-        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+        set_tile(monkeypatch, tile)
         dx = bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, ws)
         assert rel(dx, ref) <= TOL[dtype], name
         results[name] = dx
