@@ -47,6 +47,14 @@ def fused_max_rows() -> int:
     return int(v) if v not in (None, "") else _DEFAULT_FUSED_MAX_ROWS
 
 
+def _mm_scaled(a: torch.Tensor, b: torch.Tensor, scaling: float) -> torch.Tensor:
+    """scaling * (a @ b) with the factor applied in the GEMM's epilogue (no
+    separate elementwise pass; none at all for scaling == 1)."""
+    if scaling == 1.0:
+        return a @ b
+    return torch.addmm(a.new_empty(()), a, b, beta=0, alpha=scaling)  # beta = 0: the input is never read
+
+
 class _NF4LinearFn(torch.autograd.Function):
     """y = x . W^T (+ bias) (+ scaling * (x . A^T) . B^T) with W frozen in NF4."""
 
@@ -54,7 +62,7 @@ class _NF4LinearFn(torch.autograd.Function):
     def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused):
         t = None
         if lora_a is not None:
-            t = (x.reshape(-1, x.shape[-1]) @ lora_a.t().to(x.dtype)) * scaling
+            t = _mm_scaled(x.reshape(-1, x.shape[-1]), lora_a.t().to(x.dtype), scaling)
         if fused:
             y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
                              lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
@@ -76,7 +84,7 @@ class _NF4LinearFn(torch.autograd.Function):
         dy2 = dy.reshape(-1, N).contiguous()
         u = None
         if lora_a is not None:
-            u = (dy2 @ lora_b.to(dy2.dtype)) * ctx.scaling                  # [M, R]
+            u = _mm_scaled(dy2, lora_b.to(dy2.dtype), ctx.scaling)          # [M, R]
         dx = None
         if ctx.needs_input_grad[0]:
             if ctx.fused:
