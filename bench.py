@@ -508,9 +508,9 @@ def run_mlp(torch, args):
 
 
 def run_small_m(torch, args):
-    """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward and
-    input gradient, whose few output tiles get a split reduction, against
-    dequantize + hipBLASLt."""
+    """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward (the
+    weight-streaming small-M kernel plus its split reduce) and input gradient
+    (split reduction over the tile kernel), against dequantize + hipBLASLt."""
     from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd
     dev = torch.device("cuda:0")
     N, K, M = 14336, 4096, 16
@@ -556,6 +556,29 @@ def run_profile(args):
     print(json.dumps({"profile": "done", "reps": args.kernel_reps, "copy_bytes": 4 * src.numel()}), flush=True)
 
 
+def run_profile_small_m(args):
+    """Kernel-only pass for rocprofv3 at decode size: the fused forward (small-M
+    kernel + split reduce) and input gradient at M = 16 on the 14336 x 4096
+    weight, each launched --kernel-reps times."""
+    import torch
+
+    from stratum_amd.functional import nf4_gemm_bwd_dx, nf4_gemm_fwd
+
+    dev = torch.device("cuda:0")
+    N, K, M = 14336, 4096, 16
+    p, st = _gpu_quantized(torch, (N, K), 40, dev)
+    x = seeded(torch, (M, K), 41, 1.0, torch.bfloat16, dev)
+    dy = seeded(torch, (M, N), 42, 1.0, torch.bfloat16, dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    for _ in range(args.kernel_reps):
+        nf4_gemm_fwd(x, p, st.absmax, (N, K), 64, out=y)
+    for _ in range(args.kernel_reps):
+        nf4_gemm_bwd_dx(dy, p, st.absmax, (N, K), 64, out=dx)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "small_m16 done", "reps": args.kernel_reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -569,6 +592,8 @@ def main():
     ap.add_argument("--layers", type=int, default=32, help="decoder layers in the stream-in config")
     ap.add_argument("--profile", action="store_true",
                     help="launch each kernel --kernel-reps times for rocprofv3; prints no bench line")
+    ap.add_argument("--profile-small-m", action="store_true",
+                    help="as --profile, for the M = 16 forward and input gradient")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -578,6 +603,9 @@ def main():
         sys.exit(2)
     if args.profile:
         run_profile(args)
+        return
+    if args.profile_small_m:
+        run_profile_small_m(args)
         return
     line = run_lora_step(args)
     print(json.dumps(line), flush=True)
