@@ -105,6 +105,11 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
     __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
                      : "memory", "m0");
 }
+// 4 bytes global -> LDS for every lane; destination lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds_base) {
+    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_base), "v"(src)
+                     : "memory", "m0");
+}
 // The same copy from a wave-uniform 64-bit base plus a 32-bit per-lane byte offset
 // (global_load_lds with an SGPR base: no 64-bit address arithmetic per copy).
 __device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_t lds_base) {
@@ -1337,129 +1342,190 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 
 // ------------------------------------------------------------ small-M forward
 // Y[M, N] = X[M, K] . W[N, K]^T for M <= 16 rows (decode-sized batches),
-// where streaming the weight, not the MFMA, is the bound. Each wave owns
-// 16 R weight rows (R tiles of v_mfma_f32_16x16x32, weight rows x activation
-// rows) over one reduction range; the weight-side operand is dequantized in
-// registers as in k_gemm_fwd_rw and the activation operand comes straight from
-// memory, shared by the R tiles. A 128-deep chunk: lane (r = lane % 16,
-// h = lane / 16) loads 16 packed bytes (k = 32 h + 0..31) of row r of each
-// tile and one absmax, and MFMA q (0..3) of the chunk takes k = 32 h + 8 q +
-// (0..7) from both operands, so every load instruction reads 64 contiguous
-// bytes of each of 16 rows. The bound is the L1 access rate: the operand
-// layout puts neighbouring lanes on different rows, so each lane's 16 bytes
-// cost an access of their own. K % 128 == 64 leaves the upper half of the last chunk empty: those
-// lanes read the row start with a zero scale and zero activations. Reduction
-// ranges (splits) write fp32 partials [split][m][n] that k_split_reduce sums
-// (with bias and the LoRA term); with one range the output (plus bias) is
-// stored directly.
-#ifndef STM_GEMV_U
-#define STM_GEMV_U 2
-#endif
-#ifndef STM_GEMV_WAVES
-#define STM_GEMV_WAVES 4
-#endif
-template <typename Tr, int R>
-__global__ __launch_bounds__(64 * STM_GEMV_WAVES) void k_gemv_fwd(GemmArgs g, int chunks_per_split) {
-    constexpr int U = STM_GEMV_U;
+// bound by streaming the weight. A work-group of 8 waves owns 256 weight rows
+// (32 per wave, two v_mfma_f32_16x16x32 tiles of weight rows x activation
+// rows) over one reduction range, walked in groups of 256. Every operand
+// reaches LDS through lane-contiguous global -> LDS copies (whole cache lines,
+// one L1 access per line), double-buffered, one barrier per group:
+//  - packed weight: each wave copies its own 32 rows x 128 bytes (8 lanes per
+//    row); the 16-byte piece p of row r sits in slot p ^ ((r >> 1) & 7), so
+//    the MFMA-layout reads (16 lanes = 16 rows, same piece) hit all banks once;
+//  - absmax: each wave copies its rows' blocks of the group (dword copies);
+//  - activations: the group's <= 16 rows x 512 bytes, shared by the waves,
+//    piece p of row m in slot p ^ m.
+// Within a group, 128-deep chunk c (0, 1): lane (r = lane % 16, h = lane / 16)
+// reads 16 packed bytes (k = 128 c + 32 h + 0..31) of row r of each tile and
+// their absmax, dequantizes in registers with the level table as in
+// k_gemm_fwd_rw, and MFMA q (0..3) takes k = 128 c + 32 h + 8 q + (0..7) from
+// both operands. Past K (K % 256 != 0) the copies read valid addresses and
+// the lanes use a zero scale and zero activations. Reduction ranges (splits)
+// write fp32 partials [split][m][n] that k_split_reduce sums (with bias and
+// the LoRA term); with one range the output (plus bias) is stored directly.
+constexpr int GV_WAVES = 8, GV_R = 2, GV_ROWS = 16 * GV_R * GV_WAVES, GV_GK = 256;
+
+template <typename Tr>
+__global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
+    constexpr int R = GV_R;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    __shared__ float2 lut_all[256 * RW_LUT_COPIES];
-    fill_lut_rw<64 * STM_GEMV_WAVES>(lut_all, tid);
-    __syncthreads();
+    // one LDS array, the level table first (at address 0, so a perm-built
+    // table address needs no base added)
+    constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = 16 * 32 * 16, kW = GV_WAVES * 32 * 8 * 16, kA = GV_WAVES * 32 * 4 * 4;
+    __shared__ __align__(16) uint8_t smem[kLut + 2 * (kX + kW + kA)];
+    float2* lut_all = reinterpret_cast<float2*>(smem);
+    auto sx = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + buf * kX); };
+    auto sw = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + 2 * kX + buf * kW) + wave * 256; };
+    auto sa = [&](int buf) { return reinterpret_cast<float*>(smem + kLut + 2 * (kX + kW) + buf * kA) + wave * 128; };
 
     const int64_t K = g.K, N = g.N, M = g.M;
     const int bshift = 31 - __builtin_clz(g.blocksize);
-    const int64_t n0 = ((int64_t)blockIdx.x * STM_GEMV_WAVES + wave) * (16 * R);
+    const int nfl = (GV_GK >> bshift) > 0 ? (GV_GK >> bshift) : 1;  // absmax per row per group
+    const int64_t kblocks = K >> bshift;
+    const int ngroups = (int)((K + GV_GK - 1) / GV_GK);
     const int z = blockIdx.y;
-    const int nchunks = (int)((K + 127) / 128);
-    const int c_begin = z * chunks_per_split;
-    int c_end = c_begin + chunks_per_split;
-    c_end = c_end < nchunks ? c_end : nchunks;
-    const int r = lane & 15, h = lane >> 4;
-    const uint8_t* wrow[R];
-    const float* arow[R];
-#pragma unroll
-    for (int t = 0; t < R; ++t) {
-        int64_t n = n0 + 16 * t + r;
-        n = n < N ? n : N - 1;
-        wrow[t] = g.packed + n * (K / 2);
-        arow[t] = g.absmax + n * (K >> bshift);
-    }
-    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(g.a) + (r < M ? r : M - 1) * K;
-    const uint32_t lut_base = (uint32_t)(size_t)((const __attribute__((address_space(3))) float2*)lut_all);
-    const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
+    const int g_begin = z * groups_per_split;
+    const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
+    const int64_t nw0 = (int64_t)blockIdx.x * GV_ROWS + wave * 32;  // this wave's first weight row
 
+    // copy sources (per lane; group offsets added per copy)
+    const uint8_t* wsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        const int64_t n = nw0 + row < N ? nw0 + row : N - 1;
+        wsrc[i] = g.packed + n * (K / 2) + 16 * ((lane & 7) ^ ((row >> 1) & 7));
+    }
+    const int a_rows_per_copy = 64 / nfl, a_copies = (32 * nfl + 63) / 64;
+    const float* asrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t n0 = nw0 + lane / nfl + i * a_rows_per_copy;
+        asrc[i] = g.absmax + (n0 < N ? n0 : N - 1) * kblocks;
+    }
+    const int aj = lane % nfl;
+    const int xm = 2 * wave + (lane >> 5);  // activation row this lane copies (8 waves x 2 rows)
+    const uint16_t* xsrc = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
+    const int xpiece = (lane & 31) ^ (xm & 15);
+
+    auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
+    auto copy_group = [&](int grp, int buf) {
+        const int64_t kg = (int64_t)grp * GV_GK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // bytes past the row (K % 256 != 0) read the row start instead
+            const int piece = (lane & 7) ^ (((8 * i + (lane >> 3)) >> 1) & 7);
+            const uint8_t* src = kg / 2 + 16 * piece < K / 2 ? wsrc[i] + kg / 2 : wsrc[i] - 16 * piece;
+            dma16(src, uniform(lds_offset(sw(buf) + i * 64)));
+        }
+        const int64_t b0 = kg >> bshift;
+        const int64_t blk = b0 + aj < kblocks ? b0 + aj : kblocks - 1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (i < a_copies)
+                dma4(asrc[i] + blk,
+                     uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(sa(buf) + i * 64))));
+        const int64_t k = kg + 8 * xpiece;
+        dma16(xsrc + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * wave * 32)));
+    };
+
+    const int r = lane & 15, h = lane >> 4;
+    const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
     f32x4_t acc[R];
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // U chunks per group: all loads of a group, then its dequantization and
-    // MFMAs; other waves of the CU hide the latency
-    for (int c0 = c_begin; c0 < c_end; c0 += U) {
-        uint4 q[U][R];
-        float a[U][R];
-        uint4 xv[U][4];
+    // one group: work items (chunk c, tile t) in order i = 2 c + t; the table
+    // reads of item i + 1 are issued before item i's products, conversions and
+    // MFMAs. TAIL (the group that reaches past K) zeroes the activations and
+    // the scale of lanes whose k is past K.
+    auto compute = [&](int buf, int grp, auto tail_c) {
+        constexpr bool TAIL = decltype(tail_c)::value;
+        uint4 xv[2][4], qv[2 * R];
+        float av[2 * R];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u;
-            const int k = 128 * c + 32 * h;
-            // chunks past the range and the empty half of a last chunk read
-            // the row start and contribute zeros
-            const bool ok = c < c_end && k < K;
-            const int64_t wo = ok ? k / 2 : 0, xo = ok ? k : 0;
-            const int ai = ok ? (k >> bshift) : 0;
+        for (int c = 0; c < 2; ++c) {
+            const bool ok = !TAIL || (int64_t)grp * GV_GK + 128 * c + 32 * h < K;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = sx(buf)[r * 32 + ((16 * c + 4 * h + q) ^ r)];
+                xv[c][q] = ok ? v : make_uint4(0, 0, 0, 0);
+            }
+            const int blk = (128 * c + 32 * h) >> bshift;
 #pragma unroll
             for (int t = 0; t < R; ++t) {
-                q[u][t] = *reinterpret_cast<const uint4*>(wrow[t] + wo);
-                const float av = arow[t][ai];
-                a[u][t] = ok ? av : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint4 v = *reinterpret_cast<const uint4*>(xrow + xo + 8 * j);
-                xv[u][j] = ok ? v : make_uint4(0, 0, 0, 0);
+                const int row = 16 * t + r;
+                qv[2 * c + t] = sw(buf)[row * 8 + ((4 * c + h) ^ ((row >> 1) & 7))];
+                const float a = sa(buf)[row * nfl + blk];
+                av[2 * c + t] = ok ? a : 0.0f;
             }
         }
+        f32x2_t p[2][4][4];
+        auto issue = [&](int i, f32x2_t (&pp)[4][4]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t word = q == 0 ? qv[i].x : q == 1 ? qv[i].y : q == 2 ? qv[i].z : qv[i].w;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int t = 0; t < R; ++t) {
-                    const uint32_t word = j == 0 ? q[u][t].x : j == 1 ? q[u][t].y : j == 2 ? q[u][t].z : q[u][t].w;
-                    f32x2_t p[4];
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const uint32_t addr =
-                            __builtin_amdgcn_perm(copy_off, word, 0x0C0C0004u | ((uint32_t)b << 8));
-                        p[b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)(lut_base + addr);
-                    }
-                    const float av = a[u][t];
-                    uint4 w;
-                    w.x = Tr::pack2(opaque(p[0].x * av), opaque(p[0].y * av));
-                    w.y = Tr::pack2(opaque(p[1].x * av), opaque(p[1].y * av));
-                    w.z = Tr::pack2(opaque(p[2].x * av), opaque(p[2].y * av));
-                    w.w = Tr::pack2(opaque(p[3].x * av), opaque(p[3].y * av));
-                    acc[t] = mfma16<Tr>(w, xv[u][j], acc[t]);
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t addr = __builtin_amdgcn_perm(copy_off, word, 0x0C0C0004u | ((uint32_t)b << 8));
+                    pp[q][b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)addr;
                 }
             }
+        };
+        issue(0, p[0]);
+#pragma unroll
+        for (int i = 0; i < 2 * R; ++i) {
+            if (i + 1 < 2 * R) issue(i + 1, p[(i + 1) & 1]);
+            sched_fence();
+            const int c = i / R, t = i % R;
+            const float a = av[i];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x2_t(&pq)[4] = p[i & 1][q];
+                uint4 w;
+                w.x = Tr::pack2(opaque(pq[0].x * a), opaque(pq[0].y * a));
+                w.y = Tr::pack2(opaque(pq[1].x * a), opaque(pq[1].y * a));
+                w.z = Tr::pack2(opaque(pq[2].x * a), opaque(pq[2].y * a));
+                w.w = Tr::pack2(opaque(pq[3].x * a), opaque(pq[3].y * a));
+                acc[t] = mfma16<Tr>(w, xv[c][q], acc[t]);
+            }
+            sched_fence();
         }
+    };
+
+    if (g_begin < g_end) copy_group(g_begin, 0);  // in flight while the level table is filled
+    fill_lut_rw<64 * GV_WAVES>(lut_all, tid);
+    wait_vmem();
+    __syncthreads();  // level table and group g_begin ready
+    for (int grp = g_begin; grp < g_end; ++grp) {
+        const int buf = (grp - g_begin) & 1;
+        if (grp + 1 < g_end) copy_group(grp + 1, buf ^ 1);
+        if ((int64_t)(grp + 1) * GV_GK > K)
+            compute(buf, grp, std::true_type());
+        else
+            compute(buf, grp, std::false_type());
+        wait_vmem();
+        __syncthreads();  // group grp + 1 landed; every wave is done reading this buffer
     }
 
-    // C[4 h + i][r] of tile t: weight row n0 + 16 t + 4 h + i, activation row r
+    // C[4 h + i][r] of tile t: weight row nw0 + 16 t + 4 h + i, activation row r
     const uint16_t* bias = reinterpret_cast<const uint16_t*>(g.bias);
 #pragma unroll
     for (int t = 0; t < R; ++t) {
         const int64_t m = r;
-        const int64_t nc = n0 + 16 * t + 4 * h;
+        const int64_t nc = nw0 + 16 * t + 4 * h;
         if (m >= M || nc >= N) continue;  // N % 8 == 0: all four columns valid
         if (g.splits > 1) {
             *reinterpret_cast<float4*>(g.partial + (int64_t)z * M * N + m * N + nc) =
                 make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
         } else {
-            float v[4];
+            float v[4] = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+            if (bias) {  // 2-byte aligned: four 16-bit loads, issued together
+                uint16_t bb[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = acc[t][i] + (bias ? Tr::to_f32(bias[nc + i]) : 0.0f);
+                for (int i = 0; i < 4; ++i) bb[i] = bias[nc + i];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] += Tr::to_f32(bb[i]);
+            }
             uint2 pk;
             pk.x = Tr::pack2(v[0], v[1]);
             pk.y = Tr::pack2(v[2], v[3]);
@@ -1539,45 +1605,38 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
 #define STM_GEMV_MAX_M 16
 #endif
 
-#ifndef STM_GEMV_TARGET
-#define STM_GEMV_TARGET 2048
+#ifndef STM_GEMV_T_LAT
+#define STM_GEMV_T_LAT 3.0  // fixed cost of a work-group (copy latency, level table), in groups
 #endif
-// Small-M forward: weight row tiles per wave (4 for wide weights, where fewer
-// activation loads per weight byte pay; 2 otherwise, for more waves).
-int gemv_tiles(int64_t N) { return N >= 8192 ? 4 : 2; }
-
-// Reduction ranges so that about STM_GEMV_TARGET waves stream weights
-// (N / (16 R) waves per range), at least 4 chunks of 128 per range.
+// Small-M forward: reduction ranges (in groups of 256) that minimise
+// rounds x (fixed cost + groups per range), one work-group per CU, plus the
+// split reduce when there is more than one range.
 int gemv_splits(int64_t N, int64_t K) {
-    const int rows = 16 * gemv_tiles(N);
-    const int64_t waves = (N + rows - 1) / rows, chunks = (K + 127) / 128;
-    int64_t sp = (STM_GEMV_TARGET + waves - 1) / waves;
-    const int64_t max_sp = chunks / 4 > 1 ? chunks / 4 : 1;
-    sp = sp < max_sp ? sp : max_sp;
-    return (int)(sp < 1 ? 1 : sp);
+    const int64_t blocks = (N + GV_ROWS - 1) / GV_ROWS, groups = (K + GV_GK - 1) / GV_GK;
+    if (groups <= 1) return 1;
+    int best = 1;
+    double best_t = 1e30;
+    for (int64_t sp = 1; sp <= groups && sp <= 64; ++sp) {
+        const int64_t gps = (groups + sp - 1) / sp, spe = (groups + gps - 1) / gps;
+        const int64_t rounds = (blocks * spe + 255) / 256;
+        const double t = (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0);
+        if (t < best_t - 1e-9) best_t = t, best = (int)spe;
+    }
+    return best;
 }
 
 bool use_gemv(int64_t M, int num_groups) { return num_groups == 1 && M > 0 && M <= STM_GEMV_MAX_M; }
 
 int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
-    const int nchunks = (int)((g.K + 127) / 128);
-    const int cps = (nchunks + g.splits - 1) / g.splits;
-    const int splits = cps ? (nchunks + cps - 1) / cps : 1;  // every range non-empty (K = 0: one empty range)
+    const int ngroups = (int)((g.K + GV_GK - 1) / GV_GK);
+    const int gps = (ngroups + g.splits - 1) / g.splits;
+    const int splits = gps ? (ngroups + gps - 1) / gps : 1;  // every range non-empty (K = 0: one empty range)
     g.splits = splits;
-    const int R = gemv_tiles(g.N);
-    const int rows_per_block = 16 * R * STM_GEMV_WAVES;
-    dim3 grid((unsigned)((g.N + rows_per_block - 1) / rows_per_block), (unsigned)splits), block(64 * STM_GEMV_WAVES);
-    if (R == 4) {
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_fwd<BF16, 4>), grid, block, 0, stream, g, cps);
-        else
-            hipLaunchKernelGGL((k_gemv_fwd<F16, 4>), grid, block, 0, stream, g, cps);
-    } else {
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_fwd<BF16, 2>), grid, block, 0, stream, g, cps);
-        else
-            hipLaunchKernelGGL((k_gemv_fwd<F16, 2>), grid, block, 0, stream, g, cps);
-    }
+    dim3 grid((unsigned)((g.N + GV_ROWS - 1) / GV_ROWS), (unsigned)splits), block(64 * GV_WAVES);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL(k_gemv_fwd<BF16>, grid, block, 0, stream, g, gps);
+    else
+        hipLaunchKernelGGL(k_gemv_fwd<F16>, grid, block, 0, stream, g, gps);
     int rc = check_launch("gemm_fwd (small M)");
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.N, g.bias, dtype, stream, true);

@@ -140,13 +140,14 @@ def test_gemm_workspace_sizing(L):
     # ways over the 224 steps of its 14336-long reduction
     assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 2 * 17 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
-    # forward with M <= 16: the small-M kernel's ranges (about 2048 waves of 64
-    # weight rows for N >= 8192, else 32 rows; at least 4 chunks of 128 each):
-    # 224 waves x 8 ranges (32 chunks); 128 waves x 16 ranges
-    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 8 * 16 * 14336 * 4
-    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 16 * 1 * 4096 * 4
-    # a short reduction caps the split: 8 steps per tile-path range, 4 chunks
-    # per small-M range (both give 2 here)
+    # forward with M <= 16: the small-M kernel's ranges (blocks of 256 weight
+    # rows, one per CU; groups of 256 along K; fewest rounds x (3 + groups per
+    # range) + 6 for the reduce): 56 blocks x 16 groups -> 4 ranges of 4
+    # (224 work-groups, one round); 16 blocks x 56 groups -> 14 ranges of 4
+    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 4 * 16 * 14336 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 14 * 1 * 4096 * 4
+    # a short reduction: the small-M kernel runs one range (no workspace), the
+    # tile path (pinned tile kinds) splits 2 ways at 8 steps per range
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 256, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(0, 256, 4096, 0) == 0

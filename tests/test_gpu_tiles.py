@@ -100,12 +100,14 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (300, 256, 512, 128, True, 32),    # blocksize 128
     (64, 1000, 320, 64, False, 16),    # 1000 columns: last tile 232 wide
     (33, 2048, 4096, 256, False, 0),   # small M: split reductions exist
-    (16, 520, 576, 64, True, 16),      # small-M kernel: 520 columns, K % 128 == 64 (half-empty last chunk)
+    (16, 520, 576, 64, True, 16),      # small-M kernel: 520 columns, K % 256 == 64 (half-empty last chunk)
     (5, 4096, 1024, 128, True, 32),    # small-M kernel, blocksize 128, bias + LoRA in the reduce
-    (12, 264, 4160, 64, False, 16),    # small-M kernel: 33 chunks over uneven ranges
+    (12, 264, 4160, 64, False, 16),    # small-M kernel: 17 groups of 256 over uneven ranges
     (15, 8, 64, 64, True, 0),          # one half chunk, eight columns, unsplit with bias
-    (3, 8192, 320, 64, True, 0),       # four row tiles per wave, unsplit, half-empty last chunk
-    (9, 8200, 1024, 256, True, 16),    # four row tiles per wave, split, last block partly outside
+    (3, 8192, 320, 64, True, 0),       # unsplit, K % 256 == 64
+    (9, 8200, 1024, 256, True, 16),    # split, last block of 256 weight rows partly outside
+    (7, 264, 384, 128, True, 0),       # K % 256 == 128: last group's second chunk empty
+    (11, 520, 448, 64, False, 0),      # K % 256 == 192: last group's second chunk half empty
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
