@@ -1544,29 +1544,52 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
     const int64_t total = rows * (cols / 4), plane = rows * cols;
     for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < total; v += (int64_t)gridDim.x * blockDim.x) {
         const int64_t e = v * 4;
+        // partials summed in split order; four loads in flight at a time
         float4 acc = *reinterpret_cast<const float4*>(partial + e);
-        for (int z = 1; z < splits; ++z) {
+        int z = 1;
+        for (; z + 4 <= splits; z += 4) {
+            float4 p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = *reinterpret_cast<const float4*>(partial + (z + i) * plane + e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc.x += p[i].x;
+                acc.y += p[i].y;
+                acc.z += p[i].z;
+                acc.w += p[i].w;
+            }
+        }
+        for (; z < splits; ++z) {
             const float4 p = *reinterpret_cast<const float4*>(partial + z * plane + e);
             acc.x += p.x;
             acc.y += p.y;
             acc.z += p.z;
             acc.w += p.w;
         }
-        if (R > 0) {
+        if (R > 0) {  // R % 16 == 0; T, L 16-byte aligned: 8 ranks per load
             const int64_t row = e / cols, c = e % cols;
-            const uint16_t* t = T + row * R;
-            float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
-            for (int k = 0; k < R; ++k) {
-                const float tk = Tr::to_f32(t[k]);
-                l0 += tk * Tr::to_f32(L[(c + 0) * R + k]);
-                l1 += tk * Tr::to_f32(L[(c + 1) * R + k]);
-                l2 += tk * Tr::to_f32(L[(c + 2) * R + k]);
-                l3 += tk * Tr::to_f32(L[(c + 3) * R + k]);
+            const uint4* t8 = reinterpret_cast<const uint4*>(T + row * R);
+            float l[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int k8 = 0; k8 < R / 8; ++k8) {
+                const uint4 tv = t8[k8];
+                uint4 lv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) lv[i] = reinterpret_cast<const uint4*>(L + (c + i) * R)[k8];
+                const uint32_t tw[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lw[4] = {lv[i].x, lv[i].y, lv[i].z, lv[i].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        l[i] += Tr::to_f32((uint16_t)(tw[j] & 0xFFFF)) * Tr::to_f32((uint16_t)(lw[j] & 0xFFFF));
+                        l[i] += Tr::to_f32((uint16_t)(tw[j] >> 16)) * Tr::to_f32((uint16_t)(lw[j] >> 16));
+                    }
+                }
             }
-            acc.x += l0;
-            acc.y += l1;
-            acc.z += l2;
-            acc.w += l3;
+            acc.x += l[0];
+            acc.y += l[1];
+            acc.z += l[2];
+            acc.w += l[3];
         }
         if (bias) {
             const int64_t c = e % cols;
