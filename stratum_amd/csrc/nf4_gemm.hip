@@ -1361,7 +1361,12 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 // the lanes use a zero scale and zero activations. Reduction ranges (splits)
 // write fp32 partials [split][m][n] that k_split_reduce sums (with bias and
 // the LoRA term); with one range the output (plus bias) is stored directly.
-constexpr int GV_WAVES = 8, GV_R = 2, GV_ROWS = 16 * GV_R * GV_WAVES, GV_GK = 256;
+#ifndef STM_GEMV_WAVES
+#define STM_GEMV_WAVES 8
+#endif
+// 256 weight rows per work-group: waves x tiles of 16 rows = 16
+constexpr int GV_WAVES = STM_GEMV_WAVES, GV_R = 16 / GV_WAVES, GV_RW = 16 * GV_R, GV_ROWS = 256, GV_GK = 256;
+static_assert(GV_WAVES * GV_R == 16, "256 weight rows per work-group");
 
 template <typename Tr>
 __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
@@ -1370,12 +1375,12 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // one LDS array, the level table first (at address 0, so a perm-built
     // table address needs no base added)
-    constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = 16 * 32 * 16, kW = GV_WAVES * 32 * 8 * 16, kA = GV_WAVES * 32 * 4 * 4;
+    constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = 16 * 32 * 16, kW = GV_ROWS * 8 * 16, kA = GV_ROWS * 4 * 4;
     __shared__ __align__(16) uint8_t smem[kLut + 2 * (kX + kW + kA)];
     float2* lut_all = reinterpret_cast<float2*>(smem);
     auto sx = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + buf * kX); };
-    auto sw = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + 2 * kX + buf * kW) + wave * 256; };
-    auto sa = [&](int buf) { return reinterpret_cast<float*>(smem + kLut + 2 * (kX + kW) + buf * kA) + wave * 128; };
+    auto sw = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + 2 * kX + buf * kW) + wave * (GV_RW * 8); };
+    auto sa = [&](int buf) { return reinterpret_cast<float*>(smem + kLut + 2 * (kX + kW) + buf * kA) + wave * (GV_RW * 4); };
 
     const int64_t K = g.K, N = g.N, M = g.M;
     const int bshift = 31 - __builtin_clz(g.blocksize);
@@ -1385,33 +1390,40 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
     const int z = blockIdx.y;
     const int g_begin = z * groups_per_split;
     const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
-    const int64_t nw0 = (int64_t)blockIdx.x * GV_ROWS + wave * 32;  // this wave's first weight row
+    const int64_t nw0 = (int64_t)blockIdx.x * GV_ROWS + wave * GV_RW;  // this wave's first weight row
 
     // copy sources (per lane; group offsets added per copy)
-    const uint8_t* wsrc[4];
+    const uint8_t* wsrc[2 * R];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2 * R; ++i) {
         const int row = 8 * i + (lane >> 3);
         const int64_t n = nw0 + row < N ? nw0 + row : N - 1;
         wsrc[i] = g.packed + n * (K / 2) + 16 * ((lane & 7) ^ ((row >> 1) & 7));
     }
-    const int a_rows_per_copy = 64 / nfl, a_copies = (32 * nfl + 63) / 64;
-    const float* asrc[2];
+    const int a_rows_per_copy = 64 / nfl, a_copies = (GV_RW * nfl + 63) / 64;  // <= R
+    const float* asrc[R];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < R; ++i) {
         const int64_t n0 = nw0 + lane / nfl + i * a_rows_per_copy;
         asrc[i] = g.absmax + (n0 < N ? n0 : N - 1) * kblocks;
     }
     const int aj = lane % nfl;
-    const int xm = 2 * wave + (lane >> 5);  // activation row this lane copies (8 waves x 2 rows)
-    const uint16_t* xsrc = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
-    const int xpiece = (lane & 31) ^ (xm & 15);
+    // activations: 8 copies of two rows each, copy ix by wave ix % GV_WAVES
+    constexpr int XC = GV_WAVES >= 8 ? 1 : 8 / GV_WAVES;
+    const uint16_t* xsrc[XC];
+    int xpiece[XC];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int xm = 2 * (wave + j * GV_WAVES) + (lane >> 5);  // activation row this lane copies
+        xsrc[j] = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
+        xpiece[j] = (lane & 31) ^ (xm & 15);
+    }
 
     auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
     auto copy_group = [&](int grp, int buf) {
         const int64_t kg = (int64_t)grp * GV_GK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2 * R; ++i) {
             // bytes past the row (K % 256 != 0) read the row start instead
             const int piece = (lane & 7) ^ (((8 * i + (lane >> 3)) >> 1) & 7);
             const uint8_t* src = kg / 2 + 16 * piece < K / 2 ? wsrc[i] + kg / 2 : wsrc[i] - 16 * piece;
@@ -1420,12 +1432,16 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
         const int64_t b0 = kg >> bshift;
         const int64_t blk = b0 + aj < kblocks ? b0 + aj : kblocks - 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < R; ++i)
             if (i < a_copies)
                 dma4(asrc[i] + blk,
                      uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(sa(buf) + i * 64))));
-        const int64_t k = kg + 8 * xpiece;
-        dma16(xsrc + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * wave * 32)));
+#pragma unroll
+        for (int j = 0; j < XC; ++j)
+            if (wave + j * GV_WAVES < 8) {
+                const int64_t k = kg + 8 * xpiece[j];
+                dma16(xsrc[j] + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * (wave + j * GV_WAVES) * 32)));
+            }
     };
 
     const int r = lane & 15, h = lane >> 4;
@@ -1434,7 +1450,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // one group: work items (chunk c, tile t) in order i = 2 c + t; the table
+    // one group: work items (chunk c, tile t) in order i = R c + t; the table
     // reads of item i + 1 are issued before item i's products, conversions and
     // MFMAs. TAIL (the group that reaches past K) zeroes the activations and
     // the scale of lanes whose k is past K.
@@ -1454,9 +1470,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
 #pragma unroll
             for (int t = 0; t < R; ++t) {
                 const int row = 16 * t + r;
-                qv[2 * c + t] = sw(buf)[row * 8 + ((4 * c + h) ^ ((row >> 1) & 7))];
+                qv[R * c + t] = sw(buf)[row * 8 + ((4 * c + h) ^ ((row >> 1) & 7))];
                 const float a = sa(buf)[row * nfl + blk];
-                av[2 * c + t] = ok ? a : 0.0f;
+                av[R * c + t] = ok ? a : 0.0f;
             }
         }
         f32x2_t p[2][4][4];
