@@ -1830,17 +1830,19 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
     return t;
 }
 
-// The 128 x 256 register-weight tile (kMid) as a cost-model choice for the input
-// gradient: measured at M = 512..4096 on the 14336 x 4096 and 4096 x 14336
-// weights it is 0-12 % faster than the choices without it there; for the
-// forward it measured -3..+5 %, so the forward uses it only when pinned
-// (STRATUM_NF4_GEMM_TILE=mid). Per-step times calibrated at M = 4096, N = 2048,
-// K = 1024..4096 (256 tiles): forward 1.28 us, input gradient 1.08 us.
+// The 128 x 256 register-weight tile (kMid) as a cost-model choice (unsplit
+// only). Input gradient: measured at M = 512..4096 on the 14336 x 4096 and
+// 4096 x 14336 weights it is 0-12 % faster than the choices without it.
+// Forward: it pays only where its tiles fill the GPU and the big tiles do not
+// (M = 4096 on W [2048, 1024]: 32.9 us against 40.6); the per-step time is
+// calibrated with every CU busy (1.55 us; 1.2-1.3 us on a half-empty GPU), so
+// the model does not pick it on the 8B-class weights at M = 256..2048, where
+// it measured -3..+5 %. Input gradient per step 1.1 us.
 #ifndef STM_MID_TILE
 #define STM_MID_TILE 1
 #endif
 #ifndef STM_T_MID_FWD
-#define STM_T_MID_FWD 1.3
+#define STM_T_MID_FWD 1.55  // per step with every CU busy (1.2-1.3 on a half-empty GPU)
 #endif
 #ifndef STM_T_MID_BWD
 #define STM_T_MID_BWD 1.1
@@ -1896,7 +1898,7 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
             best_t = ts;
             best = Plan{kSmall, small_tiles, sp};
         }
-        if (sp == 1 && (STM_MID_TILE || only == kMid) && (backward || only == kMid)) {
+        if (sp == 1 && (STM_MID_TILE || only == kMid)) {
             const double tm = plan_cost(mid_tiles, steps, 1, t_mid, M, cols);
             if ((only < 0 || only == kMid) && tm < best_t) {
                 best_t = tm;
