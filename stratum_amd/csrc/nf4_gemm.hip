@@ -372,6 +372,70 @@ __device__ __forceinline__ void store_tile_f32(const f32x16_t (&acc)[FA][FB], fl
     }
 }
 
+#ifndef STM_RW_LDS_STORE
+#define STM_RW_LDS_STORE 1
+#endif
+// Output tile through LDS: each wave writes its slice (32 FA columns x 32 FB
+// rows, NP passes of 32 FB / NP rows) into a private LDS stage (rows of CH =
+// 4 FA chunks of 16 bytes, chunk slot c ^ (row % CH)), then stores it with
+// 16-byte lanes, CH lanes per output row, so every store instruction writes
+// whole cache lines. Direct stores from the accumulator layout write 8 bytes
+// per lane across 32 rows and cost about a tenth of a 64-step 256 x 256 tile.
+// The caller has made the stage free (barrier) and frees it for others after
+// (barrier). ocols % 8 == 0. CX = 1: accumulator row r holds column r ^ 1.
+template <typename Tr, int FA, int FB, int CX = 0, int NP = 2>
+__device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
+                                               int ocol_base, int ocols, int orow_base, int orows,
+                                               const uint16_t* __restrict__ bias, int lane, uint4* stage) {
+    static_assert(FB % NP == 0 && (FA == 2 || FA == 4), "64 or 128 columns per wave");
+    // (the register-weight kernels use FA = 2, NP = 2; the LDS-weight kernels'
+    // 128 x 128 tiles store a quarter of the bytes per item and measured no gain)
+    constexpr int FP = FB / NP, RP = 32 * FP, CH = 4 * FA, RPI = 64 / CH;  // rows per pass / per store
+    const int hi = lane >> 5, c0 = ocol_base + 4 * hi;
+    float bv[FA][4][4];
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int col = c0 + i * 32 + 8 * q + (e ^ CX);
+                bv[i][q][e] = (bias && col < ocols) ? Tr::to_f32(bias[col]) : 0.0f;
+            }
+    uint8_t* st = reinterpret_cast<uint8_t*>(stage);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int jj = 0; jj < FP; ++jj) {
+            const int rr = 32 * jj + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < FA; ++i) {
+                f32x16_t a = acc[i][p * FP + jj];
+                __asm__ volatile("" : "+v"(a));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = a[4 * q + e] + bv[i][q][e];
+                    uint2 pk;
+                    pk.x = CX ? Tr::pack2(v[1], v[0]) : Tr::pack2(v[0], v[1]);
+                    pk.y = CX ? Tr::pack2(v[3], v[2]) : Tr::pack2(v[2], v[3]);
+                    const int slot = (4 * i + q) ^ (rr & (CH - 1));
+                    *reinterpret_cast<uint2*>(st + rr * (16 * CH) + slot * 16 + 8 * hi) = pk;
+                }
+            }
+        }
+        // 16-byte lanes: row rr = RPI it + lane / CH, chunk lane % CH
+#pragma unroll
+        for (int it = 0; it < RP / RPI; ++it) {
+            const int rr = RPI * it + lane / CH, c = lane % CH;
+            const uint4 v = stage[rr * CH + (c ^ (rr & (CH - 1)))];
+            const int orow = orow_base + p * RP + rr, col = ocol_base + 8 * c;
+            if (orow < orows && col < ocols) *reinterpret_cast<uint4*>(out + (orow * ld + col)) = v;
+        }
+    }
+}
+
 // Step range of split z of `steps` reduction steps.
 __device__ __forceinline__ void split_range(int steps, int splits, int z, int& begin, int& count) {
     begin = (int)(((int64_t)z * steps) / splits);
@@ -766,64 +830,6 @@ __device__ __forceinline__ void store_tile_rw(const f32x16_t (&acc)[FA][FB], uin
     }
 }
 
-// store_tile_rw through LDS: each wave writes its 64-column slice, half of its
-// rows at a time, into a private LDS stage (RP rows x 8 chunks of 16 bytes,
-// chunk slot c ^ (row & 7)), then stores it with 16-byte lanes, 8 lanes per
-// 128-byte output row, so every store instruction writes 8 whole cache lines
-// (direct stores from the accumulator layout write 8 bytes per lane across 32
-// rows and cost about a tenth of a 64-step tile). The caller has made the
-// stage free (barrier) and frees it for others after (barrier). FA == 2.
-template <typename Tr, int FA, int FB, int CX = 0>
-__device__ __forceinline__ void store_tile_rw_lds(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
-                                                  int ocol_base, int ocols, int orow_base, int orows,
-                                                  const uint16_t* __restrict__ bias, int lane, uint4* stage) {
-    static_assert(FA == 2 && FB % 2 == 0, "64 columns per wave, two passes");
-    constexpr int FP = FB / 2, RP = 32 * FP;  // fragments and rows per pass
-    const int hi = lane >> 5, c0 = ocol_base + 4 * hi;
-    float bv[FA][4][4];
-#pragma unroll
-    for (int i = 0; i < FA; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int col = c0 + i * 32 + 8 * q + (e ^ CX);
-                bv[i][q][e] = (bias && col < ocols) ? Tr::to_f32(bias[col]) : 0.0f;
-            }
-    uint8_t* st = reinterpret_cast<uint8_t*>(stage);
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-#pragma unroll
-        for (int jj = 0; jj < FP; ++jj) {
-            const int rr = 32 * jj + (lane & 31);
-#pragma unroll
-            for (int i = 0; i < FA; ++i) {
-                f32x16_t a = acc[i][p * FP + jj];
-                __asm__ volatile("" : "+v"(a));
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = a[4 * q + e] + bv[i][q][e];
-                    uint2 pk;
-                    pk.x = CX ? Tr::pack2(v[1], v[0]) : Tr::pack2(v[0], v[1]);
-                    pk.y = CX ? Tr::pack2(v[3], v[2]) : Tr::pack2(v[2], v[3]);
-                    const int slot = (4 * i + q) ^ (rr & 7);
-                    *reinterpret_cast<uint2*>(st + rr * 128 + slot * 16 + 8 * hi) = pk;
-                }
-            }
-        }
-        // 16-byte lanes: row rr = 8 it + lane / 8, chunk lane % 8
-#pragma unroll
-        for (int it = 0; it < RP / 8; ++it) {
-            const int rr = 8 * it + (lane >> 3), c = lane & 7;
-            const uint4 v = stage[rr * 8 + (c ^ (rr & 7))];
-            const int orow = orow_base + p * RP + rr, col = ocol_base + 8 * c;
-            if (orow < orows && col < ocols) *reinterpret_cast<uint4*>(out + (orow * ld + col)) = v;
-        }
-    }
-}
-
 // fp32 partial tile of one split for the register-weight kernels: the mapping of
 // store_tile_rw (CX as there), 16-byte runs, 32-bit offsets within the split's
 // [rows][ld] slice.
@@ -859,9 +865,6 @@ __device__ __forceinline__ void store_tile_f32_rw(const f32x16_t (&acc)[FA][FB],
     }
 }
 
-#ifndef STM_RW_LDS_STORE
-#define STM_RW_LDS_STORE 1
-#endif
 // Instruction order of one sub-step of the register-weight kernels: SLOTS
 // slots of 1 MFMA, 2 VALU (dequantization) and 1 LDS read (activation
 // fragment or level table), an order the compiler's scheduler must follow.
@@ -1001,7 +1004,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
         constexpr int RPW = 16 * FB * 8, PER_BUF = BM * 8 / RPW;
         uint4* stage = (wave < PER_BUF ? sA0 + wave * RPW : sA1 + (wave - PER_BUF) * RPW);
         __syncthreads();  // every wave is done reading the activation buffers
-        store_tile_rw_lds<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
+        store_tile_lds<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
                                      (int)N, (int)(m0 + xrow0), (int)grp.rows,
                                      reinterpret_cast<const uint16_t*>(g.bias), lane_e, stage);
     } else {
@@ -1410,7 +1413,7 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
         constexpr int RPW = 16 * FB * 8, PER_BUF = BM * 8 / RPW;
         uint4* stage = (wave < PER_BUF ? sA0 + wave * RPW : sA1 + (wave - PER_BUF) * RPW);
         __syncthreads();  // every wave is done reading the dY buffers
-        store_tile_rw_lds<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
+        store_tile_lds<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
                                         (int)K, (int)m0, (int)grp.rows, nullptr, lane_e, stage);
     } else {
         store_tile_rw<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
