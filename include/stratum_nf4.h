@@ -95,7 +95,10 @@ int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, in
  *                  When the problem has too few output tiles to fill the GPU
  *                  (small M) the reduction is split over several work-groups
  *                  whose fp32 partials go there and are summed (in a fixed
- *                  order) by a second kernel; NULL disables the split.
+ *                  order) by a second kernel; NULL disables the split. For
+ *                  M <= 16 a weight-streaming kernel runs instead of the tiles
+ *                  when it has this workspace (or needs none: one range and no
+ *                  LoRA term); its split reduce adds bias and the LoRA term.
  *   constraints  : K % 64 == 0, K % blocksize == 0, all pointers 16-byte aligned
  */
 int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
