@@ -96,7 +96,7 @@ int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, in
  *                  (small M) the reduction is split over several work-groups
  *                  whose fp32 partials go there and are summed (in a fixed
  *                  order) by a second kernel; NULL disables the split. For
- *                  M <= 16 a weight-streaming kernel runs instead of the tiles
+ *                  M <= 32 a weight-streaming kernel runs instead of the tiles
  *                  when it has this workspace (or needs none: one range and no
  *                  LoRA term); its split reduce adds bias and the LoRA term.
  *   constraints  : K % 64 == 0, K % blocksize == 0, all pointers 16-byte aligned

@@ -251,14 +251,16 @@ __device__ __forceinline__ float level_from_immediates(int i) {
 // would put a dozen dependent round trips at the start of every block).
 template <int NT, int COPIES>
 __device__ __forceinline__ void fill_level_table(float2* lut, int tid) {
-    static_assert((256 * COPIES) % NT == 0, "every thread writes the same number of entries");
+    constexpr int ENTRIES = 256 * COPIES, ITERS = (ENTRIES + NT - 1) / NT;
     const int mine = __float_as_int(level_from_immediates(tid & 15));
 #pragma unroll
-    for (int i = 0; i < 256 * COPIES / NT; ++i) {
-        const int t = tid + NT * i, b = t / COPIES;
+    for (int i = 0; i < ITERS; ++i) {
+        // every lane takes part in the gathers; a last partial pass (NT not
+        // dividing the table) only skips the write
+        const int t = tid + NT * i, b = (t < ENTRIES ? t : ENTRIES - 1) / COPIES;
         const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((b >> 4) << 2, mine));
         const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((b & 15) << 2, mine));
-        lut[t] = make_float2(hi, lo);
+        if (ENTRIES % NT == 0 || t < ENTRIES) lut[t] = make_float2(hi, lo);
     }
 }
 
@@ -1444,26 +1446,36 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 // the lanes use a zero scale and zero activations. Reduction ranges (splits)
 // write fp32 partials [split][m][n] that k_split_reduce sums (with bias and
 // the LoRA term); with one range the output (plus bias) is stored directly.
-#ifndef STM_GEMV_WAVES
-#define STM_GEMV_WAVES 8
-#endif
-// 256 weight rows per work-group: waves x tiles of 16 rows = 16
-constexpr int GV_WAVES = STM_GEMV_WAVES, GV_R = 16 / GV_WAVES, GV_RW = 16 * GV_R, GV_ROWS = 256, GV_GK = 256;
-static_assert(GV_WAVES * GV_R == 16, "256 weight rows per work-group");
+// Work-group shape of the small-M forward for up to 16 MB activation rows:
+// WAVES waves of 32 weight rows (two 16-row MFMA tiles) each. MB = 1: 8 waves
+// (256 rows); MB = 2: 6 waves (192 rows), so the doubled activation buffers
+// still fit beside the 64 KB level table (150 KB of LDS).
+template <int MB>
+struct GvCfg {
+    static constexpr int WAVES = MB == 1 ? 8 : 6, R = 2, RW = 32, ROWS = RW * WAVES, XR = 16 * MB, GK = 256;
+    static constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = XR * 32 * 16, kW = ROWS * 8 * 16, kA = ROWS * 4 * 4;
+    static constexpr int kLds = kLut + 2 * (kX + kW + kA);
+    static_assert(kLds <= 160 * 1024, "LDS");
+};
+constexpr int GV_GK = 256;
 
-template <typename Tr>
-__global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
-    constexpr int R = GV_R;
+template <typename Tr, int MB>
+__global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
+    using C = GvCfg<MB>;
+    constexpr int R = C::R, WAVES = C::WAVES;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // one LDS array, the level table first (at address 0, so a perm-built
     // table address needs no base added)
-    constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = 16 * 32 * 16, kW = GV_ROWS * 8 * 16, kA = GV_ROWS * 4 * 4;
-    __shared__ __align__(16) uint8_t smem[kLut + 2 * (kX + kW + kA)];
+    __shared__ __align__(16) uint8_t smem[C::kLds];
     float2* lut_all = reinterpret_cast<float2*>(smem);
-    auto sx = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + buf * kX); };
-    auto sw = [&](int buf) { return reinterpret_cast<uint4*>(smem + kLut + 2 * kX + buf * kW) + wave * (GV_RW * 8); };
-    auto sa = [&](int buf) { return reinterpret_cast<float*>(smem + kLut + 2 * (kX + kW) + buf * kA) + wave * (GV_RW * 4); };
+    auto sx = [&](int buf) { return reinterpret_cast<uint4*>(smem + C::kLut + buf * C::kX); };
+    auto sw = [&](int buf) {
+        return reinterpret_cast<uint4*>(smem + C::kLut + 2 * C::kX + buf * C::kW) + wave * (C::RW * 8);
+    };
+    auto sa = [&](int buf) {
+        return reinterpret_cast<float*>(smem + C::kLut + 2 * (C::kX + C::kW) + buf * C::kA) + wave * (C::RW * 4);
+    };
 
     const int64_t K = g.K, N = g.N, M = g.M;
     const int bshift = 31 - __builtin_clz(g.blocksize);
@@ -1473,7 +1485,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
     const int z = blockIdx.y;
     const int g_begin = z * groups_per_split;
     const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
-    const int64_t nw0 = (int64_t)blockIdx.x * GV_ROWS + wave * GV_RW;  // this wave's first weight row
+    const int64_t nw0 = (int64_t)blockIdx.x * C::ROWS + wave * C::RW;  // this wave's first weight row
 
     // copy sources (per lane; group offsets added per copy)
     const uint8_t* wsrc[2 * R];
@@ -1483,7 +1495,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
         const int64_t n = nw0 + row < N ? nw0 + row : N - 1;
         wsrc[i] = g.packed + n * (K / 2) + 16 * ((lane & 7) ^ ((row >> 1) & 7));
     }
-    const int a_rows_per_copy = 64 / nfl, a_copies = (GV_RW * nfl + 63) / 64;  // <= R
+    const int a_rows_per_copy = 64 / nfl, a_copies = (C::RW * nfl + 63) / 64;  // <= R
     const float* asrc[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -1491,13 +1503,13 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
         asrc[i] = g.absmax + (n0 < N ? n0 : N - 1) * kblocks;
     }
     const int aj = lane % nfl;
-    // activations: 8 copies of two rows each, copy ix by wave ix % GV_WAVES
-    constexpr int XC = GV_WAVES >= 8 ? 1 : 8 / GV_WAVES;
+    // activations: XR / 2 copies of two rows each, copy ix by wave ix % WAVES
+    constexpr int XI = C::XR / 2, XC = (XI + WAVES - 1) / WAVES;
     const uint16_t* xsrc[XC];
     int xpiece[XC];
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
-        const int xm = 2 * (wave + j * GV_WAVES) + (lane >> 5);  // activation row this lane copies
+        const int xm = 2 * (wave + j * WAVES) + (lane >> 5);  // activation row this lane copies
         xsrc[j] = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
         xpiece[j] = (lane & 31) ^ (xm & 15);
     }
@@ -1521,17 +1533,19 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
                      uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(sa(buf) + i * 64))));
 #pragma unroll
         for (int j = 0; j < XC; ++j)
-            if (wave + j * GV_WAVES < 8) {
+            if (wave + j * WAVES < XI) {
                 const int64_t k = kg + 8 * xpiece[j];
-                dma16(xsrc[j] + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * (wave + j * GV_WAVES) * 32)));
+                dma16(xsrc[j] + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * (wave + j * WAVES) * 32)));
             }
     };
 
     const int r = lane & 15, h = lane >> 4;
     const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
-    f32x4_t acc[R];
+    f32x4_t acc[R][MB];
 #pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // one group: work items (chunk c, tile t) in order i = R c + t; the table
     // reads of item i + 1 are issued before item i's products, conversions and
@@ -1539,16 +1553,19 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
     // the scale of lanes whose k is past K.
     auto compute = [&](int buf, int grp, auto tail_c) {
         constexpr bool TAIL = decltype(tail_c)::value;
-        uint4 xv[2][4], qv[2 * R];
+        uint4 xv[2][MB][4], qv[2 * R];
         float av[2 * R];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const bool ok = !TAIL || (int64_t)grp * GV_GK + 128 * c + 32 * h < K;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = sx(buf)[r * 32 + ((16 * c + 4 * h + q) ^ r)];
-                xv[c][q] = ok ? v : make_uint4(0, 0, 0, 0);
-            }
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int xr = 16 * mb + r;
+                    const uint4 v = sx(buf)[xr * 32 + ((16 * c + 4 * h + q) ^ r)];
+                    xv[c][mb][q] = ok ? v : make_uint4(0, 0, 0, 0);
+                }
             const int blk = (128 * c + 32 * h) >> bshift;
 #pragma unroll
             for (int t = 0; t < R; ++t) {
@@ -1585,14 +1602,15 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
                 w.y = Tr::pack2(opaque(pq[1].x * a), opaque(pq[1].y * a));
                 w.z = Tr::pack2(opaque(pq[2].x * a), opaque(pq[2].y * a));
                 w.w = Tr::pack2(opaque(pq[3].x * a), opaque(pq[3].y * a));
-                acc[t] = mfma16<Tr>(w, xv[c][q], acc[t]);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[t][mb] = mfma16<Tr>(w, xv[c][mb][q], acc[t][mb]);
             }
             sched_fence();
         }
     };
 
     if (g_begin < g_end) copy_group(g_begin, 0);  // in flight while the level table is filled
-    fill_lut_rw<64 * GV_WAVES>(lut_all, tid);
+    fill_lut_rw<64 * WAVES>(lut_all, tid);
     wait_vmem();
     __syncthreads();  // level table and group g_begin ready
     for (int grp = g_begin; grp < g_end; ++grp) {
@@ -1606,31 +1624,33 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_fwd(GemmArgs g, int grou
         __syncthreads();  // group grp + 1 landed; every wave is done reading this buffer
     }
 
-    // C[4 h + i][r] of tile t: weight row nw0 + 16 t + 4 h + i, activation row r
+    // C[4 h + i][r] of tile t, block mb: weight row nw0 + 16 t + 4 h + i, activation row 16 mb + r
     const uint16_t* bias = reinterpret_cast<const uint16_t*>(g.bias);
 #pragma unroll
-    for (int t = 0; t < R; ++t) {
-        const int64_t m = r;
-        const int64_t nc = nw0 + 16 * t + 4 * h;
-        if (m >= M || nc >= N) continue;  // N % 8 == 0: all four columns valid
-        if (g.splits > 1) {
-            *reinterpret_cast<float4*>(g.partial + (int64_t)z * M * N + m * N + nc) =
-                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-        } else {
-            float v[4] = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
-            if (bias) {  // 2-byte aligned: four 16-bit loads, issued together
-                uint16_t bb[4];
+    for (int t = 0; t < R; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) bb[i] = bias[nc + i];
+        for (int mb = 0; mb < MB; ++mb) {
+            const int64_t m = 16 * mb + r;
+            const int64_t nc = nw0 + 16 * t + 4 * h;
+            if (m >= M || nc >= N) continue;  // N % 8 == 0: all four columns valid
+            if (g.splits > 1) {
+                *reinterpret_cast<float4*>(g.partial + (int64_t)z * M * N + m * N + nc) =
+                    make_float4(acc[t][mb][0], acc[t][mb][1], acc[t][mb][2], acc[t][mb][3]);
+            } else {
+                float v[4] = {acc[t][mb][0], acc[t][mb][1], acc[t][mb][2], acc[t][mb][3]};
+                if (bias) {  // 2-byte aligned: four 16-bit loads, issued together
+                    uint16_t bb[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] += Tr::to_f32(bb[i]);
+                    for (int i = 0; i < 4; ++i) bb[i] = bias[nc + i];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] += Tr::to_f32(bb[i]);
+                }
+                uint2 pk;
+                pk.x = Tr::pack2(v[0], v[1]);
+                pk.y = Tr::pack2(v[2], v[3]);
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * N + nc) = pk;
             }
-            uint2 pk;
-            pk.x = Tr::pack2(v[0], v[1]);
-            pk.y = Tr::pack2(v[2], v[3]);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * N + nc) = pk;
         }
-    }
 }
 
 // Sum of the split partials [splits][rows][cols] (+ bias) (+ T[row] . L[col]
@@ -1723,18 +1743,22 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
     return check_launch("gemm split reduce");
 }
 
+
 #ifndef STM_GEMV_MAX_M
-#define STM_GEMV_MAX_M 16
+#define STM_GEMV_MAX_M 32
 #endif
 
 #ifndef STM_GEMV_T_LAT
 #define STM_GEMV_T_LAT 3.0  // fixed cost of a work-group (copy latency, level table), in groups
 #endif
+int gemv_rows_per_block(int64_t M) { return M <= 16 ? GvCfg<1>::ROWS : GvCfg<2>::ROWS; }
+
 // Small-M forward: reduction ranges (in groups of 256) that minimise
 // rounds x (fixed cost + groups per range), one work-group per CU, plus the
 // split reduce when there is more than one range.
-int gemv_splits(int64_t N, int64_t K) {
-    const int64_t blocks = (N + GV_ROWS - 1) / GV_ROWS, groups = (K + GV_GK - 1) / GV_GK;
+int gemv_splits(int64_t M, int64_t N, int64_t K) {
+    const int64_t rows = gemv_rows_per_block(M);
+    const int64_t blocks = (N + rows - 1) / rows, groups = (K + GV_GK - 1) / GV_GK;
     if (groups <= 1) return 1;
     int best = 1;
     double best_t = 1e30;
@@ -1754,11 +1778,21 @@ int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
     const int gps = (ngroups + g.splits - 1) / g.splits;
     const int splits = gps ? (ngroups + gps - 1) / gps : 1;  // every range non-empty (K = 0: one empty range)
     g.splits = splits;
-    dim3 grid((unsigned)((g.N + GV_ROWS - 1) / GV_ROWS), (unsigned)splits), block(64 * GV_WAVES);
-    if (dtype == STM_BF16)
-        hipLaunchKernelGGL(k_gemv_fwd<BF16>, grid, block, 0, stream, g, gps);
-    else
-        hipLaunchKernelGGL(k_gemv_fwd<F16>, grid, block, 0, stream, g, gps);
+    const int rows = gemv_rows_per_block(g.M);
+    dim3 grid((unsigned)((g.N + rows - 1) / rows), (unsigned)splits);
+    if (g.M <= 16) {
+        dim3 block(64 * GvCfg<1>::WAVES);
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, 1>), grid, block, 0, stream, g, gps);
+        else
+            hipLaunchKernelGGL((k_gemv_fwd<F16, 1>), grid, block, 0, stream, g, gps);
+    } else {
+        dim3 block(64 * GvCfg<2>::WAVES);
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, 2>), grid, block, 0, stream, g, gps);
+        else
+            hipLaunchKernelGGL((k_gemv_fwd<F16, 2>), grid, block, 0, stream, g, gps);
+    }
     int rc = check_launch("gemm_fwd (small M)");
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.N, g.bias, dtype, stream, true);
@@ -2002,7 +2036,7 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
     // small M: room for either kernel (a pinned tile kind skips the small-M one)
     int64_t gemv_need = 0;
     if (!backward && use_gemv(M, num_groups)) {
-        const int sp = gemv_splits(N, K);
+        const int sp = gemv_splits(M, N, K);
         gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
     }
     const int sp = gemm_splits(M, N, K, backward, num_groups);
@@ -2015,7 +2049,7 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     // small M: the weight-streaming kernel, when its partials have a workspace
     // (or it needs none) and the LoRA term can go to the reduce
     if (use_gemv(g.M, g.num_groups) && tile_override() < 0) {
-        const int sp = gemv_splits(g.N, g.K);
+        const int sp = gemv_splits(g.M, g.N, g.K);
         if (sp == 1 ? g.lora_rank == 0 : g.partial != nullptr) {
             g.splits = sp;
             return launch_gemv_fwd(g, dtype, stream);

@@ -135,10 +135,10 @@ def test_gemm_workspace_sizing(L):
     # large problems fill the GPU with output tiles: no split, no workspace
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 1) == 0
-    # M = 17, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
+    # M = 33, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
     # M = 16: the input gradient's 16 big tiles (4096 output columns) split 16
     # ways over the 224 steps of its 14336-long reduction
-    assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 2 * 17 * 14336 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(33, 14336, 4096, 0) == 2 * 33 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
     # forward with M <= 16: the small-M kernel's ranges (blocks of 256 weight
     # rows, one per CU; groups of 256 along K; fewest rounds x (3 + groups per
@@ -146,6 +146,9 @@ def test_gemm_workspace_sizing(L):
     # (224 work-groups, one round); 16 blocks x 56 groups -> 14 ranges of 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 4 * 16 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 14 * 1 * 4096 * 4
+    # 17..32 rows: blocks of 192 weight rows: 75 blocks x 16 groups -> 3 ranges
+    # of 6 (225 work-groups, one round)
+    assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 3 * 17 * 14336 * 4
     # a short reduction: the small-M kernel runs one range (no workspace), the
     # tile path (pinned tile kinds) splits 2 ways at 8 steps per range
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4

@@ -3,7 +3,7 @@
 The library picks, per call, the 256 x 256 tile (register-weight kernels, or
 LDS-weight kernels for some split reductions), the 128 x 256 register-weight
 tile (unsplit) or the 128 x 128 LDS-weight tile, split or not, and for a
-forward of at most 16 rows the weight-streaming small-M kernel (its reduction
+forward of at most 32 rows the weight-streaming small-M kernel (its reduction
 ranges summed by the split-reduce kernel, which adds bias and the LoRA term).
 STRATUM_NF4_GEMM_TILE pins the tile kind (and so skips the small-M kernel) and
 a call through the C ABI without a workspace pins "unsplit", so each kernel is
@@ -108,6 +108,10 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (9, 8200, 1024, 256, True, 16),    # split, last block of 256 weight rows partly outside
     (7, 264, 384, 128, True, 0),       # K % 256 == 128: last group's second chunk empty
     (11, 520, 448, 64, False, 0),      # K % 256 == 192: last group's second chunk half empty
+    (17, 8, 64, 64, True, 0),          # 32-row variant: one half chunk, unsplit with bias
+    (24, 520, 576, 64, True, 16),      # 32-row variant, split, LoRA in the reduce
+    (31, 200, 448, 64, True, 0),       # 32-row variant, blocks of 192 rows (second partial), K % 256 == 192
+    (32, 4104, 4160, 64, False, 16),   # 32-row variant, uneven ranges
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
