@@ -1426,18 +1426,19 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 }
 
 // ------------------------------------------------------------ small-M forward
-// Y[M, N] = X[M, K] . W[N, K]^T for M <= 16 rows (decode-sized batches),
-// bound by streaming the weight. A work-group of 8 waves owns 256 weight rows
-// (32 per wave, two v_mfma_f32_16x16x32 tiles of weight rows x activation
-// rows) over one reduction range, walked in groups of 256. Every operand
+// Y[M, N] = X[M, K] . W[N, K]^T for M <= 32 rows (decode-sized batches),
+// bound by dequantizing the streamed weight. A work-group owns 32 weight rows
+// per wave (two v_mfma_f32_16x16x32 tiles of weight rows x activation rows,
+// 16 MB activation rows; GvCfg) over one reduction range, walked in groups of
+// 256. Every operand
 // reaches LDS through lane-contiguous global -> LDS copies (whole cache lines,
 // one L1 access per line), double-buffered, one barrier per group:
 //  - packed weight: each wave copies its own 32 rows x 128 bytes (8 lanes per
 //    row); the 16-byte piece p of row r sits in slot p ^ ((r >> 1) & 7), so
 //    the MFMA-layout reads (16 lanes = 16 rows, same piece) hit all banks once;
 //  - absmax: each wave copies its rows' blocks of the group (dword copies);
-//  - activations: the group's <= 16 rows x 512 bytes, shared by the waves,
-//    piece p of row m in slot p ^ m.
+//  - activations: the group's <= 16 MB rows x 512 bytes, shared by the waves,
+//    piece p of row m in slot p ^ (m % 16).
 // Within a group, 128-deep chunk c (0, 1): lane (r = lane % 16, h = lane / 16)
 // reads 16 packed bytes (k = 128 c + 32 h + 0..31) of row r of each tile and
 // their absmax, dequantizes in registers with the level table as in
