@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define STM_NF4_ABI_VERSION 2
+#define STM_NF4_ABI_VERSION 3
 
 /* return codes */
 #define STM_OK 0
@@ -166,6 +166,32 @@ int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const flo
 int stm_swiglu_fwd(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype, void* stream);
 int stm_swiglu_bwd(const void* grad_out, const void* gate_up, void* grad_gate_up, int64_t rows, int64_t inter,
                    int dtype, void* stream);
+
+/*
+ * Rank-R side products of a LoRA adapter on the frozen NF4 base. They replace the
+ * autograd matmuls of PEFT's lora.Linear (the adapter the reference attaches
+ * in scripts/train.py:568-573; forward lora_B(lora_A(x)) * scaling):
+ *   stm_lora_down: T[M, R]  = scaling * X[M, K] . A[R, K]^T          (forward, lora_A)
+ *   stm_lora_dy:   U[M, R]  = scaling * dY[M, N] . B[N, R]           (backward, into lora_B)
+ *                  dB[N, R] = dY^T . T  (skipped when dB is NULL)     (gradient of lora_B)
+ *   stm_lora_da:   dA[R, K] = U^T . X                                (gradient of lora_A)
+ * T and U are the rank-R tensors the fused GEMMs take as lora_x. stm_lora_dy
+ * reads dY once for both U and dB. fp32 accumulation; the fp32 partial sums of
+ * the column/row blocks go to the caller's workspace and are added in a fixed
+ * order (deterministic), scaled and rounded once. R in {8, 16, 24, 32}; the
+ * column count of the large operand (K or N) a multiple of 8; all operands
+ * 16-byte aligned, row-major and contiguous; dtype STM_BF16 or STM_F16.
+ * Workspace: stm_lora_workspace_bytes(rows, cols, R, op) bytes, 16-byte aligned,
+ * op 0 = down (rows M, cols K), 1 = dy (M, N) with dB, 2 = da (M, K); for
+ * stm_lora_dy without dB, op 1 also suffices. Asynchronous on `stream`.
+ */
+int64_t stm_lora_workspace_bytes(int64_t rows, int64_t cols, int rank, int op);
+int stm_lora_down(const void* X, const void* A, void* T, int64_t M, int64_t K, int rank, float scaling, int dtype,
+                  void* workspace, int64_t workspace_bytes, void* stream);
+int stm_lora_dy(const void* dY, const void* B, const void* T, void* U, void* dB, int64_t M, int64_t N, int rank,
+                float scaling, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+int stm_lora_da(const void* U, const void* X, void* dA, int64_t M, int64_t K, int rank, int dtype, void* workspace,
+                int64_t workspace_bytes, void* stream);
 
 /*
  * Host-only introspection used by the CPU test suite (no GPU work):

@@ -10,7 +10,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libstratum_nf4.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["nf4_abi.hip", "nf4_quant.hip", "nf4_gemm.hip", "swiglu.hip"]
+SOURCES = ["nf4_abi.hip", "nf4_quant.hip", "nf4_gemm.hip", "swiglu.hip", "lora.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

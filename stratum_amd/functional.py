@@ -384,3 +384,95 @@ def swiglu_bwd(grad_out: torch.Tensor, gate_up: torch.Tensor, out: Optional[torc
                                        _lib.stream_handle(dev))
     _lib.check(rc, "stm_swiglu_bwd")
     return dgu.reshape(*gate_up.shape[:-1], two_i)
+
+
+# ------------------------------------------------------------ LoRA side products
+LORA_RANKS = (8, 16, 24, 32)
+
+
+def lora_supported(rank: int, cols: int) -> bool:
+    """Ranks and column counts (K or N of the frozen weight) the LoRA kernels take."""
+    return rank in LORA_RANKS and cols % 8 == 0
+
+
+def _lora_workspace(rows: int, cols: int, rank: int, op: int, device) -> Optional[torch.Tensor]:
+    nbytes = int(_lib.lib().stm_lora_workspace_bytes(rows, cols, rank, op))
+    if nbytes < 0:
+        _lib.check(nbytes, "stm_lora_workspace_bytes")
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return t.data_ptr() if t is not None and t.numel() else None
+
+
+@torch.no_grad()
+def lora_down(x: torch.Tensor, lora_a: torch.Tensor, scaling: float = 1.0) -> torch.Tensor:
+    """``scaling * x @ lora_a.T`` as [rows, R] in x's dtype (the ``T`` the fused
+    forward takes as ``lora_t``); one pass over x, fp32 accumulation, one rounding."""
+    K = x.shape[-1]
+    R = int(lora_a.shape[0])
+    tag = _gemm_dtype(x)
+    if tuple(lora_a.shape) != (R, K):
+        raise ValueError(f"lora_a shape {tuple(lora_a.shape)} != ({R}, {K})")
+    M = 1
+    for d in x.shape[:-1]:
+        M *= int(d)
+    x2 = _aligned(x.reshape(M, K))
+    a = _aligned(lora_a.to(x.dtype))
+    dev = x2.device
+    t = torch.empty((M, R), dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        ws = _lora_workspace(M, K, R, 0, dev)
+        rc = _lib.lib().stm_lora_down(_ptr(x2), _ptr(a), _ptr(t), M, K, R, float(scaling), tag, _ptr(ws),
+                                      4 * ws.numel() if ws is not None else 0, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_lora_down")
+    return t
+
+
+@torch.no_grad()
+def lora_dy(dy: torch.Tensor, lora_b: torch.Tensor, t: Optional[torch.Tensor] = None, scaling: float = 1.0):
+    """``(scaling * dy @ lora_b, dy.T @ t)`` -- the rank-R input of the LoRA term of
+    dX and the gradient of ``lora_b`` -- from one pass over dy. The second is None
+    when ``t`` is None. Results in dy's dtype."""
+    N = dy.shape[-1]
+    R = int(lora_b.shape[1])
+    tag = _gemm_dtype(dy)
+    if tuple(lora_b.shape) != (N, R):
+        raise ValueError(f"lora_b shape {tuple(lora_b.shape)} != ({N}, {R})")
+    d2 = _aligned(dy.reshape(-1, N))
+    b = _aligned(lora_b.to(dy.dtype))
+    M = d2.shape[0]
+    dev = d2.device
+    t2 = None
+    if t is not None:
+        t2 = _aligned(t.reshape(M, R).to(dy.dtype))
+    u = torch.empty((M, R), dtype=dy.dtype, device=dev)
+    db = torch.empty((N, R), dtype=dy.dtype, device=dev) if t is not None else None
+    with torch.cuda.device(dev):
+        ws = _lora_workspace(M, N, R, 1, dev)
+        rc = _lib.lib().stm_lora_dy(_ptr(d2), _ptr(b), _ptr(t2), _ptr(u), _ptr(db), M, N, R, float(scaling), tag,
+                                    _ptr(ws), 4 * ws.numel() if ws is not None else 0, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_lora_dy")
+    return u, db
+
+
+@torch.no_grad()
+def lora_da(u: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """``u.T @ x`` ([R, K], x's dtype): the gradient of ``lora_a``; one pass over x."""
+    K = x.shape[-1]
+    x2 = _aligned(x.reshape(-1, K))
+    M = x2.shape[0]
+    R = int(u.shape[-1])
+    tag = _gemm_dtype(x)
+    u2 = _aligned(u.reshape(M, R).to(x.dtype))
+    dev = x2.device
+    da = torch.empty((R, K), dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        ws = _lora_workspace(M, K, R, 2, dev)
+        rc = _lib.lib().stm_lora_da(_ptr(u2), _ptr(x2), _ptr(da), M, K, R, tag, _ptr(ws),
+                                    4 * ws.numel() if ws is not None else 0, _lib.stream_handle(dev))
+    _lib.check(rc, "stm_lora_da")
+    return da

@@ -36,7 +36,8 @@ import torch.nn.functional as F
 
 import os
 
-from .functional import (QuantState, dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd)
+from .functional import (QuantState, dequantize_4bit, fused_supported, lora_da, lora_down, lora_dy, lora_supported,
+                         nf4_gemm_bwd_dx, nf4_gemm_fwd)
 
 _DEFAULT_FUSED_MAX_ROWS = 512
 
@@ -62,7 +63,10 @@ class _NF4LinearFn(torch.autograd.Function):
     def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused):
         t = None
         if lora_a is not None:
-            t = _mm_scaled(x.reshape(-1, x.shape[-1]), lora_a.t().to(x.dtype), scaling)
+            if lora_supported(lora_a.shape[0], x.shape[-1]):
+                t = lora_down(x, lora_a, scaling)
+            else:
+                t = _mm_scaled(x.reshape(-1, x.shape[-1]), lora_a.t().to(x.dtype), scaling)
         if fused:
             y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
                              lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
@@ -82,9 +86,15 @@ class _NF4LinearFn(torch.autograd.Function):
         x, packed, absmax, lora_a, lora_b, t = ctx.saved_tensors
         N, K = ctx.shape
         dy2 = dy.reshape(-1, N).contiguous()
-        u = None
+        u = d_b = None
         if lora_a is not None:
-            u = _mm_scaled(dy2, lora_b.to(dy2.dtype), ctx.scaling)          # [M, R]
+            if lora_supported(lora_a.shape[0], N):
+                # one pass over dY for U and (when B trains) dB
+                u, d_b = lora_dy(dy2, lora_b, t if ctx.needs_input_grad[7] else None, ctx.scaling)
+            else:
+                u = _mm_scaled(dy2, lora_b.to(dy2.dtype), ctx.scaling)      # [M, R]
+                if ctx.needs_input_grad[7]:
+                    d_b = dy2.t() @ t                                       # [N, R]
         dx = None
         if ctx.needs_input_grad[0]:
             if ctx.fused:
@@ -98,13 +108,14 @@ class _NF4LinearFn(torch.autograd.Function):
                     dx = dx + u @ lora_a.to(dy2.dtype)
             dx = dx.reshape(*dy.shape[:-1], K)
         d_bias = dy2.sum(0).to(dy.dtype) if ctx.has_bias_grad else None
-        d_a = d_b = None
+        d_a = None
         if lora_a is not None:
             x2 = x.reshape(-1, K)
             if ctx.needs_input_grad[6]:
-                d_a = (u.t() @ x2).to(lora_a.dtype)                         # [R, K]
-            if ctx.needs_input_grad[7]:
-                d_b = (dy2.t() @ t).to(lora_b.dtype)                        # [N, R]
+                d_a = lora_da(u, x2) if lora_supported(lora_a.shape[0], K) else u.t() @ x2  # [R, K]
+                d_a = d_a.to(lora_a.dtype)
+            if d_b is not None:
+                d_b = d_b.to(lora_b.dtype)
         return dx, None, None, None, None, d_bias, d_a, d_b, None, None
 
 

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version(L):
-    assert L.stm_nf4_abi_version() == 2
+    assert L.stm_nf4_abi_version() == 3
 
 
 @pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
@@ -162,3 +162,49 @@ def test_gemm_rejects_small_workspace(L):
     need = L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0)
     assert L.stm_nf4_gemm_fwd(p, p, p, None, None, None, 0, p, 16, 14336, 4096, 64, 1, p, need - 4, None) == -1
     assert b"workspace" in L.stm_last_error()
+
+
+def test_lora_arguments_are_rejected_without_a_gpu(L):
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    ws_need = L.stm_lora_workspace_bytes(64, 256, 16, 0)
+    # rank outside {8, 16, 24, 32}
+    assert L.stm_lora_down(p, p, p, 64, 256, 12, 1.0, 1, p, ws_need, None) == -2
+    assert "rank" in _err(L)
+    assert L.stm_lora_down(p, p, p, 64, 256, 64, 1.0, 1, p, ws_need, None) == -2
+    # columns not a multiple of 8
+    assert L.stm_lora_down(p, p, p, 64, 250, 16, 1.0, 1, p, ws_need, None) == -2
+    # fp32 and unknown dtypes
+    assert L.stm_lora_down(p, p, p, 64, 256, 16, 1.0, 2, p, ws_need, None) == -1
+    # misaligned operand, null operand
+    assert L.stm_lora_down(p + 2, p, p, 64, 256, 16, 1.0, 1, p, ws_need, None) == -1
+    assert L.stm_lora_dy(p, None, p, p, p, 64, 256, 16, 1.0, 1, p, 1 << 30, None) == -1
+    assert L.stm_lora_da(p, p, None, 64, 256, 16, 1, p, 1 << 30, None) == -1
+    # workspace too small or missing
+    assert L.stm_lora_down(p, p, p, 64, 256, 16, 1.0, 1, p, ws_need - 16, None) == -1
+    assert "workspace" in _err(L)
+    assert L.stm_lora_da(p, p, p, 64, 256, 16, 1, None, 0, None) == -1
+    # no rows: nothing to do for the forward product
+    assert L.stm_lora_down(None, None, None, 0, 256, 16, 1.0, 1, None, 0, None) == 0
+    assert L.stm_lora_workspace_bytes(64, 256, 16, 3) < 0
+    assert L.stm_lora_workspace_bytes(64, 256, 40, 0) < 0
+
+
+def test_lora_workspace_sizing(L):
+    """fp32 partials: [column blocks of 256][rows][RP] for the row-direction sums
+    and [row blocks][cols][RP] for the column-direction sums, RP = rank rounded
+    up to 16; about 512 work-groups (row blocks of whole 64-row steps)."""
+    # lora_dy at the 8192 x 14336 shape: 56 column blocks, 10 row blocks of 832 rows
+    assert L.stm_lora_workspace_bytes(8192, 14336, 16, 1) == 56 * 8192 * 16 * 4 + 10 * 14336 * 16 * 4
+    # lora_down / lora_da on X [8192, 4096]: 16 column blocks, 32 row blocks of 256 rows
+    assert L.stm_lora_workspace_bytes(8192, 4096, 16, 0) == 16 * 8192 * 16 * 4
+    assert L.stm_lora_workspace_bytes(8192, 4096, 16, 2) == 32 * 4096 * 16 * 4
+    # rank 8 is padded to 16, rank 24 to 32
+    assert L.stm_lora_workspace_bytes(8192, 4096, 8, 0) == 16 * 8192 * 16 * 4
+    assert L.stm_lora_workspace_bytes(8192, 4096, 24, 0) == 16 * 8192 * 32 * 4
+    # ragged: 1000 columns = 4 blocks; 65 rows = 2 steps, one row block each
+    assert L.stm_lora_workspace_bytes(65, 1000, 16, 1) == 4 * 65 * 16 * 4 + 2 * 1000 * 16 * 4
+    assert L.stm_lora_workspace_bytes(0, 1000, 16, 1) == 0
+    # no columns: nothing to reduce (a zero-width X gives T = 0)
+    assert L.stm_lora_workspace_bytes(5, 0, 16, 0) == 0
+    assert L.stm_lora_workspace_bytes(5, 0, 16, 2) == 0
