@@ -178,16 +178,19 @@ def test_nf4_linear_forward_backward(cuda, dtype, path, monkeypatch):
 
 
 @pytest.mark.parametrize("path", sorted(PATHS))
-def test_nf4_lora_linear_gradients(cuda, path, monkeypatch):
+@pytest.mark.parametrize("r,dtype", [(16, torch.bfloat16), (32, torch.float16), (8, torch.bfloat16),
+                                     (48, torch.bfloat16)])
+def test_nf4_lora_linear_gradients(cuda, path, monkeypatch, r, dtype):
+    """Rank 16 and 32 take the fused kernels' LoRA epilogues and the LoRA side
+    kernels; rank 8 takes the unfused module path; rank 48 the torch side products."""
     from stratum_amd.functional import quantize_4bit
     from stratum_amd.nf4_linear import NF4LoRALinear
     monkeypatch.setenv("STRATUM_NF4_FUSED_MAX_ROWS", PATHS[path])
-    dtype = torch.bfloat16
-    N, K, M, r = 512, 256, 160, 16
+    N, K, M = 512, 256, 160
     w = seeded((N, K), 15, 0.02, torch.float16)
     q, st = quantize_4bit(w.to(cuda))
     st.dtype = dtype
-    lin = NF4LoRALinear(q, st, r=r, lora_alpha=32.0)
+    lin = NF4LoRALinear(q, st, r=r, lora_alpha=32.0, dtype=dtype)
     with torch.no_grad():
         lin.lora_A.copy_(seeded((r, K), 16, 0.05, dtype))
         lin.lora_B.copy_(seeded((N, r), 17, 0.05, dtype))
@@ -205,10 +208,11 @@ def test_nf4_lora_linear_gradients(cuda, path, monkeypatch):
     def rel(a_, b_):
         return ((a_.float() - b_).norm() / b_.norm()).item()
 
-    assert rel(y, yr) <= 1e-2
-    assert rel(x.grad, xr.grad) <= 1e-2
-    assert rel(lin.lora_A.grad, A.grad) <= 2e-2
-    assert rel(lin.lora_B.grad, B.grad) <= 2e-2
+    tol = 1e-2 if dtype == torch.bfloat16 else 5e-3
+    assert rel(y, yr) <= tol
+    assert rel(x.grad, xr.grad) <= tol
+    assert rel(lin.lora_A.grad, A.grad) <= 2 * tol
+    assert rel(lin.lora_B.grad, B.grad) <= 2 * tol
 
 
 def test_layer_stream_materialises_each_layer_then_frees_it(cuda):
