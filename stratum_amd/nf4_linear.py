@@ -72,10 +72,16 @@ class _NF4LinearFn(torch.autograd.Function):
                              lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
         else:
             w = dequantize_4bit(packed, absmax=absmax, blocksize=blocksize, dtype=x.dtype, shape=shape)
-            y = F.linear(x, w, bias.to(x.dtype) if bias is not None else None)
-            del w
+            b = bias.to(x.dtype) if bias is not None else None
             if t is not None:
-                y = y + (t @ lora_b.to(x.dtype).t()).reshape(y.shape)
+                # rank-R term (and bias) first, then the base GEMM accumulates into it
+                # (beta = 1): no separate full-size add
+                lb_t = lora_b.to(x.dtype).t()
+                y2 = torch.addmm(b, t, lb_t) if b is not None else t @ lb_t
+                y = y2.addmm_(x.reshape(-1, x.shape[-1]), w.t()).reshape(*x.shape[:-1], w.shape[0])
+            else:
+                y = F.linear(x, w, b)
+            del w
         ctx.shape, ctx.blocksize, ctx.scaling, ctx.fused = shape, blocksize, scaling, fused
         ctx.has_bias_grad = bias is not None and bias.requires_grad
         ctx.save_for_backward(x if lora_a is not None else None, packed, absmax, lora_a, lora_b, t)
@@ -102,10 +108,11 @@ class _NF4LinearFn(torch.autograd.Function):
                                      lora_at=lora_a.t().contiguous().to(dy2.dtype) if lora_a is not None else None)
             else:
                 w = dequantize_4bit(packed, absmax=absmax, blocksize=ctx.blocksize, dtype=dy2.dtype, shape=ctx.shape)
-                dx = dy2 @ w
-                del w
                 if u is not None:
-                    dx = dx + u @ lora_a.to(dy2.dtype)
+                    dx = (u @ lora_a.to(dy2.dtype)).addmm_(dy2, w)     # rank-R term, then the base GEMM into it
+                else:
+                    dx = dy2 @ w
+                del w
             dx = dx.reshape(*dy.shape[:-1], K)
         d_bias = dy2.sum(0).to(dy.dtype) if ctx.has_bias_grad else None
         d_a = None
