@@ -248,7 +248,7 @@ def run_lora_step(args):
                     "traffic": traffic.get("k_dequantize")},
         "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
                         "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
-        "default_policy_step": {"what": "NF4LoRALinear default above 512 rows: dequantize + hipBLASLt, "
+        "default_policy_step": {"what": "NF4LoRALinear default above 768 rows: dequantize + hipBLASLt, "
                                         "backward re-dequantizes",
                                 "ms_per_step": round(default_ms, 4),
                                 "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},

@@ -6,14 +6,15 @@ whole weight to a temporary fp16 tensor and calls ``F.linear``
 (``stratum/nf4_linear.py:46-47``). Here each call picks the faster of two GPU
 paths for its row count M (tokens), measured on MI355X:
 
-* M <= ``fused_max_rows()`` (default 512): one fused dequant-GEMM forward and
+* M <= ``fused_max_rows()`` (default 768): one fused dequant-GEMM forward and
   one fused dequant-GEMM for ``dX = dY . W``; the dequantized weight never
   exists in HBM, and the packed weight (0.56 B/element) is all the weight
-  traffic -- the fused kernels win or tie there;
+  traffic -- forward plus input gradient, the fused kernels are faster there
+  (at M = 768 on the 8B-class weights: 0.22 against 0.25 ms);
 * larger M: ``dequantize_4bit`` into a temporary, then the library GEMM
-  (hipBLASLt), which is 1.3-1.5x faster than the fused kernel from M ~ 2048
-  on, because the dequantization is paid once for all rows instead of once per
-  256-row tile. The backward dequantizes again instead of keeping the
+  (hipBLASLt), whose forward is 1.2-1.3x faster than the fused kernel at
+  M = 2048..8192, because the dequantization is paid once for all rows instead
+  of once per 256-row tile. The backward dequantizes again instead of keeping the
   temporary alive (23 us for a 14336 x 4096 weight), as the reference's
   forward/recompute does.
 
@@ -39,7 +40,7 @@ import os
 from .functional import (QuantState, dequantize_4bit, fused_supported, lora_da, lora_down, lora_dy, lora_supported,
                          nf4_gemm_bwd_dx, nf4_gemm_fwd)
 
-_DEFAULT_FUSED_MAX_ROWS = 512
+_DEFAULT_FUSED_MAX_ROWS = 768
 
 
 def fused_max_rows() -> int:

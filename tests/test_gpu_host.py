@@ -244,13 +244,13 @@ def test_layer_stream_materialises_each_layer_then_frees_it(cuda):
 
 
 def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
-    """Default threshold: 512 rows fused, 513 rows through the library GEMM; both
+    """Default threshold: 768 rows fused, 769 rows through the library GEMM; both
     agree with the fp32 reference."""
     import importlib
     from stratum_amd.functional import quantize_4bit
     NL = importlib.import_module("stratum_amd.nf4_linear")  # the package exports a function of that name
     monkeypatch.delenv("STRATUM_NF4_FUSED_MAX_ROWS", raising=False)
-    assert NL.fused_max_rows() == 512
+    assert NL.fused_max_rows() == 768
     N, K = 256, 128
     w = seeded((N, K), 21, 0.02, torch.float16)
     q, st = quantize_4bit(w.to(cuda))
@@ -259,7 +259,7 @@ def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
     calls = []
     real = NL._NF4LinearFn.apply
     monkeypatch.setattr(NL._NF4LinearFn, "apply", lambda *a: calls.append(a[-1]) or real(*a))
-    for M in (512, 513):
+    for M in (768, 769):
         x = seeded((M, K), 22, 1.0, torch.bfloat16).to(cuda)
         y = NL.NF4Linear(q, st)(x)
         ref = x.float() @ wq.t().contiguous()
