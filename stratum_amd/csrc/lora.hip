@@ -342,13 +342,20 @@ __global__ __launch_bounds__(256) void k_lora_reduce(const float* __restrict__ p
 int rank_padded(int R) { return R <= 16 ? 16 : 32; }
 
 // Blocks over the rows: about two work-groups per CU of MI355X's 256 in total.
+// The buffer resource of a work-group's rows spans rows_per_block * cols * 2
+// bytes, which stays at most 2^31: the offset that marks a column outside the
+// matrix (2^31) must lie outside every range.
+constexpr int64_t kMaxRangeBytes = (int64_t)1 << 31;
+
 int64_t rows_per_block(int64_t rows, int64_t cols) {
     const int64_t ncb = cols > 0 ? (cols + LR_TN - 1) / LR_TN : 1;
     int64_t nrb = (512 + ncb - 1) / ncb;
     const int64_t steps = (rows + LR_SM - 1) / LR_SM;
     if (nrb > steps) nrb = steps;
     if (nrb < 1) nrb = 1;
-    const int64_t per = (steps + nrb - 1) / nrb;
+    int64_t per = (steps + nrb - 1) / nrb;
+    const int64_t max_per = cols > 0 ? kMaxRangeBytes / (cols * 2 * LR_SM) : per;
+    if (per > max_per) per = max_per;
     return per * LR_SM;
 }
 
@@ -413,8 +420,11 @@ int check_common(const char* what, int64_t rows, int64_t cols, int R, int dtype)
     if (dtype != STM_BF16 && dtype != STM_F16) return set_error(STM_ERR_INVALID, "%s: dtype must be bf16 or fp16", what);
     if (R < 8 || R > 32 || R % 8) return set_error(STM_ERR_UNSUPPORTED, "%s: rank %d (needs 8, 16, 24 or 32)", what, R);
     if (cols % 8) return set_error(STM_ERR_UNSUPPORTED, "%s: %lld columns (needs a multiple of 8)", what, (long long)cols);
-    if (rows > (int64_t)1 << 31 || cols > (int64_t)1 << 31)
-        return set_error(STM_ERR_UNSUPPORTED, "%s: dimension above 2^31", what);
+    // 256 rows of the large operand (a block's range plus the prefetch past it
+    // stays below 2^32) and the ROW partials of one column block (one buffer
+    // range) within kMaxRangeBytes
+    if (cols * 2 * 4 * LR_SM > kMaxRangeBytes || rows * 32 * 4 > kMaxRangeBytes)
+        return set_error(STM_ERR_UNSUPPORTED, "%s: %lld x %lld is too large", what, (long long)rows, (long long)cols);
     return STM_OK;
 }
 

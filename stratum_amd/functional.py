@@ -390,9 +390,11 @@ def swiglu_bwd(grad_out: torch.Tensor, gate_up: torch.Tensor, out: Optional[torc
 LORA_RANKS = (8, 16, 24, 32)
 
 
-def lora_supported(rank: int, cols: int) -> bool:
-    """Ranks and column counts (K or N of the frozen weight) the LoRA kernels take."""
-    return rank in LORA_RANKS and cols % 8 == 0
+def lora_supported(rank: int, cols: int, rows: int = 0) -> bool:
+    """Ranks, column counts (K or N of the frozen weight) and row counts the LoRA
+    kernels take (a 256-row slice of the large operand and the fp32 partials of
+    one 256-column block each within 2 GiB)."""
+    return rank in LORA_RANKS and cols % 8 == 0 and cols * 512 <= 1 << 31 and rows * 128 <= 1 << 31
 
 
 def _lora_workspace(rows: int, cols: int, rank: int, op: int, device) -> Optional[torch.Tensor]:

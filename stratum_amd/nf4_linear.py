@@ -64,7 +64,7 @@ class _NF4LinearFn(torch.autograd.Function):
     def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused):
         t = None
         if lora_a is not None:
-            if lora_supported(lora_a.shape[0], x.shape[-1]):
+            if lora_supported(lora_a.shape[0], x.shape[-1], x.numel() // max(x.shape[-1], 1)):
                 t = lora_down(x, lora_a, scaling)
             else:
                 t = _mm_scaled(x.reshape(-1, x.shape[-1]), lora_a.t().to(x.dtype), scaling)
@@ -95,7 +95,7 @@ class _NF4LinearFn(torch.autograd.Function):
         dy2 = dy.reshape(-1, N).contiguous()
         u = d_b = None
         if lora_a is not None:
-            if lora_supported(lora_a.shape[0], N):
+            if lora_supported(lora_a.shape[0], N, dy2.shape[0]):
                 # one pass over dY for U and (when B trains) dB
                 u, d_b = lora_dy(dy2, lora_b, t if ctx.needs_input_grad[7] else None, ctx.scaling)
             else:
@@ -120,7 +120,7 @@ class _NF4LinearFn(torch.autograd.Function):
         if lora_a is not None:
             x2 = x.reshape(-1, K)
             if ctx.needs_input_grad[6]:
-                d_a = lora_da(u, x2) if lora_supported(lora_a.shape[0], K) else u.t() @ x2  # [R, K]
+                d_a = lora_da(u, x2) if lora_supported(lora_a.shape[0], K, x2.shape[0]) else u.t() @ x2  # [R, K]
                 d_a = d_a.to(lora_a.dtype)
             if d_b is not None:
                 d_b = d_b.to(lora_b.dtype)

@@ -186,6 +186,9 @@ def test_lora_arguments_are_rejected_without_a_gpu(L):
     assert L.stm_lora_da(p, p, p, 64, 256, 16, 1, None, 0, None) == -1
     # no rows: nothing to do for the forward product
     assert L.stm_lora_down(None, None, None, 0, 256, 16, 1.0, 1, None, 0, None) == 0
+    # too large for one buffer range: 4M + 8 columns, or 2^24 + 64 rows
+    assert L.stm_lora_down(p, p, p, 64, (1 << 22) + 8, 16, 1.0, 1, p, 1 << 40, None) == -2
+    assert L.stm_lora_down(p, p, p, (1 << 24) + 64, 256, 16, 1.0, 1, p, 1 << 40, None) == -2
     assert L.stm_lora_workspace_bytes(64, 256, 16, 3) < 0
     assert L.stm_lora_workspace_bytes(64, 256, 40, 0) < 0
 
@@ -205,6 +208,11 @@ def test_lora_workspace_sizing(L):
     # ragged: 1000 columns = 4 blocks; 65 rows = 2 steps, one row block each
     assert L.stm_lora_workspace_bytes(65, 1000, 16, 1) == 4 * 65 * 16 * 4 + 2 * 1000 * 16 * 4
     assert L.stm_lora_workspace_bytes(0, 1000, 16, 1) == 0
+    # row blocks are capped so that one block of dY spans at most 2^31 bytes:
+    # 1M rows x 14336 columns -> 1170 steps of 64 rows per block, 15 row blocks
+    per = (1 << 31) // (14336 * 2 * 64)
+    nrb = -(-(1 << 20) // (per * 64))
+    assert L.stm_lora_workspace_bytes(1 << 20, 14336, 16, 2) == nrb * 14336 * 16 * 4
     # no columns: nothing to reduce (a zero-width X gives T = 0)
     assert L.stm_lora_workspace_bytes(5, 0, 16, 0) == 0
     assert L.stm_lora_workspace_bytes(5, 0, 16, 2) == 0
