@@ -106,3 +106,40 @@ def test_lora_empty_problems(cuda):
     assert u.shape == (0, 16) and db.shape == (64, 16) and not db.any()
     da = lora_da(torch.empty((0, 16), dtype=dt, device=cuda), x0)
     assert da.shape == (16, 256) and not da.any()
+
+
+def test_lora_entry_points_replay_correctly_in_a_hip_graph(cuda):
+    """T, U + dB and dA captured into one HIP graph: every replay, with eager
+    LoRA work on other inputs and synchronisations between replays, matches the
+    eager results bit for bit (the partial buffers are fully overwritten; no
+    memset is recorded)."""
+    from stratum_amd.functional import lora_da, lora_down, lora_dy
+    dt = torch.bfloat16
+    M, N, K, R = 300, 520, 264, 16
+    x = seeded((M, K), 20, 1.0, dt, cuda)
+    dy = seeded((M, N), 21, 1.0, dt, cuda)
+    a = seeded((R, K), 22, 0.05, dt, cuda)
+    b = seeded((N, R), 23, 0.05, dt, cuda)
+    t_e = lora_down(x, a, 2.0)
+    u_e, db_e = lora_dy(dy, b, t_e, 2.0)
+    da_e = lora_da(u_e, x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        lora_down(x, a, 2.0)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        t_g = lora_down(x, a, 2.0)
+        u_g, db_g = lora_dy(dy, b, t_g, 2.0)
+        da_g = lora_da(u_g, x)
+    for i in range(3):
+        junk = lora_dy(dy.flip(0), b, t_e, 0.5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(t_g, t_e), i
+        assert torch.equal(u_g, u_e) and torch.equal(db_g, db_e), i
+        assert torch.equal(da_g, da_e), i
+        del junk
