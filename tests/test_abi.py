@@ -216,3 +216,18 @@ def test_lora_workspace_sizing(L):
     # no columns: nothing to reduce (a zero-width X gives T = 0)
     assert L.stm_lora_workspace_bytes(5, 0, 16, 0) == 0
     assert L.stm_lora_workspace_bytes(5, 0, 16, 2) == 0
+
+
+def test_lora_eligibility_matches_the_library_limits(L):
+    """functional.lora_supported routes to the kernels exactly the problems the
+    library accepts (checked against the library's own answer on the CPU)."""
+    from stratum_amd.functional import lora_supported
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    cases = [(16, 14336, 8192), (8, 8, 1), (24, 4104, 130), (32, 1 << 22, 1), (16, (1 << 22) + 8, 1),
+             (16, 256, 1 << 24), (16, 256, (1 << 24) + 64), (12, 256, 64), (64, 256, 64), (16, 250, 64)]
+    for rank, cols, rows in cases:
+        rc = L.stm_lora_down(p, p, p, rows, cols, rank, 1.0, 1, p, 0, None)
+        # -1 here means only "workspace too small": the shape itself was accepted
+        accepted = rc in (0, -1)
+        assert lora_supported(rank, cols, rows) == accepted, (rank, cols, rows, rc)
