@@ -129,6 +129,17 @@ int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absm
 int64_t stm_nf4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int backward);
 
 /*
+ * Tile-shape restriction of the GEMM planner, process-wide: kind 0 = the
+ * 256 x 256 tiles, 1 = 128 x 128, 2 = 128 x 256, anything else (e.g. -1) = the
+ * cost model (the default). Starts from the environment variable
+ * STRATUM_NF4_GEMM_TILE ("big", "small", "mid"), read once when the library
+ * loads. A restriction also skips the small-M weight-streaming kernel. Returns
+ * the previous setting. Host-only. No counterpart in the reference: it lets
+ * tests reach every kernel on the same problem.
+ */
+int stm_nf4_gemm_set_tile(int kind);
+
+/*
  * Grouped fused NF4 dequant-GEMM over a stacked expert payload, forward:
  *   for each expert e: Y[off[e]:off[e+1], :] = X[off[e]:off[e+1], :] . W_e^T
  * where W is one NF4 payload of the stacked tensor [E, N, K] (the layout

@@ -354,7 +354,8 @@ int64_t rows_per_block(int64_t rows, int64_t cols) {
     if (nrb > steps) nrb = steps;
     if (nrb < 1) nrb = 1;
     int64_t per = (steps + nrb - 1) / nrb;
-    const int64_t max_per = cols > 0 ? kMaxRangeBytes / (cols * 2 * LR_SM) : per;
+    int64_t max_per = cols > 0 ? kMaxRangeBytes / (cols * 2 * LR_SM) : per;
+    if (max_per < 1) max_per = 1;  // callers reject such widths (check_common) before launching
     if (per > max_per) per = max_per;
     return per * LR_SM;
 }
@@ -451,8 +452,10 @@ int check_workspace(const char* what, const void* ws, int64_t ws_bytes, int64_t 
 using namespace stm;
 
 extern "C" int64_t stm_lora_workspace_bytes(int64_t rows, int64_t cols, int rank, int op) {
-    if (rows < 0 || cols < 0 || rank < 8 || rank > 32 || rank % 8 || op < 0 || op > 2)
-        return set_error(STM_ERR_INVALID, "lora_workspace_bytes: bad arguments");
+    if (op < 0 || op > 2) return set_error(STM_ERR_INVALID, "lora_workspace_bytes: op %d (needs 0, 1 or 2)", op);
+    // the shape limits of the entry points the workspace is for
+    const int rc = check_common("lora_workspace_bytes", rows, cols, rank, STM_BF16);
+    if (rc) return rc;
     const LoraPlan p = plan(rows, cols, rank, op != 2, op != 0);
     return p.row_bytes + p.col_bytes;
 }

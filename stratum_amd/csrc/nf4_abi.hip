@@ -90,17 +90,20 @@ int build_cell_table(int rounding, CellTable* tab) {
     return STM_OK;
 }
 
-static const CellTable* cell_table(int rounding) {
-    static CellTable tabs[2];
-    static int ready[2] = {0, 0};
-    if (rounding < 0 || rounding > 1) return nullptr;
-    if (!ready[rounding]) {  // deterministic; a racing first call just rebuilds the same bytes
-        CellTable t;
-        if (build_cell_table(rounding, &t)) return nullptr;
-        tabs[rounding] = t;
-        ready[rounding] = 1;
+// Both rules' tables, built once on first use (a function-local static: its
+// initialisation is thread-safe, so concurrent first calls see a finished table).
+struct CellTables {
+    CellTable tab[2];
+    bool ok[2];
+    CellTables() {
+        for (int r = 0; r < 2; ++r) ok[r] = build_cell_table(r, &tab[r]) == STM_OK;
     }
-    return &tabs[rounding];
+};
+
+static const CellTable* cell_table(int rounding) {
+    static const CellTables tables;
+    if (rounding < 0 || rounding > 1 || !tables.ok[rounding]) return nullptr;
+    return &tables.tab[rounding];
 }
 
 static bool is_16bit(int dt) { return dt == STM_F16 || dt == STM_BF16; }
@@ -183,6 +186,8 @@ static int check_workspace(const char* who, void* workspace, int64_t workspace_b
     if (!aligned(workspace, 16)) return set_error(STM_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
     return STM_OK;
 }
+
+int stm_nf4_gemm_set_tile(int kind) { return set_gemm_tile(kind); }
 
 int64_t stm_nf4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int backward) {
     g_err[0] = 0;

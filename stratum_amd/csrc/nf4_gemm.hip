@@ -30,6 +30,7 @@
 // MFMA layout (v_mfma_f32_32x32x16): lane l supplies A[l % 32][k-group l / 32]
 // and B[k-group l / 32][l % 32] (8 halfs each; any k order common to A and B
 // gives the same product); result v of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -1976,9 +1977,10 @@ bool rw_split_ok(bool backward, int splits, int64_t steps) {
     return backward && splits <= 4 && (steps + splits - 1) / splits >= 32;
 }
 
-// STRATUM_NF4_GEMM_TILE = "big", "mid" or "small" restricts the choice to one
-// tile kind (tests use it to reach each kernel); unset or anything else: cost model.
-int tile_override() {
+// Tile restriction: -1 = cost model, else one TileKind (tests use it to reach
+// each kernel). Starts from STRATUM_NF4_GEMM_TILE = "big", "mid" or "small",
+// read once when the library loads; stm_nf4_gemm_set_tile changes it.
+int tile_from_env() {
     const char* v = getenv("STRATUM_NF4_GEMM_TILE");
     if (!v) return -1;
     if (strcmp(v, "big") == 0) return kBig;
@@ -1986,6 +1988,10 @@ int tile_override() {
     if (strcmp(v, "mid") == 0) return kMid;
     return -1;
 }
+
+std::atomic<int> g_tile_only{tile_from_env()};
+
+int tile_override() { return g_tile_only.load(std::memory_order_relaxed); }
 
 Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t bm = backward ? STM_BWD_BM : STM_FWD_BM, bn = backward ? STM_BWD_BN : STM_FWD_BN;
@@ -2028,6 +2034,10 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
 }
 
 }  // namespace
+
+int set_gemm_tile(int kind) {
+    return g_tile_only.exchange(kind >= kBig && kind <= kMid ? kind : -1, std::memory_order_relaxed);
+}
 
 int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
     return backward ? plan(M, K, N, true, num_groups).splits : plan(M, N, K, false, num_groups).splits;

@@ -38,6 +38,10 @@ struct GemmArgs {
 int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups);
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups);
 
+// Restrict the planner to one tile kind (0 = 256 x 256, 1 = 128 x 128,
+// 2 = 128 x 256; anything else = the cost model). Returns the previous setting.
+int set_gemm_tile(int kind);
+
 int launch_quantize(const void* A, int dtype, int64_t n, int blocksize, const CellTable& tab, uint8_t* packed,
                     float* absmax, hipStream_t stream);
 int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int blocksize, void* out, int out_dtype,

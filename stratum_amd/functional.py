@@ -317,16 +317,42 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
                      expert_shape: Sequence[int], blocksize: int = 64, max_rows: Optional[int] = None,
                      backward: bool = False) -> torch.Tensor:
     """Per-expert ``x[rows_e] @ W_e.T`` (or ``@ W_e`` when ``backward``) over a stacked
-    NF4 payload of shape [E, N, K]; ``offsets`` int32 [E + 1] delimits each expert's rows."""
+    NF4 payload of shape [E, N, K]; ``offsets`` int32 [E + 1] delimits each expert's rows.
+
+    The offsets are checked on the host before any launch (one device-to-host
+    copy, the synchronisation the grid size needs anyway): ``offsets[0] == 0``,
+    non-decreasing, ``offsets[E] == x.shape[0]``; a given ``max_rows`` must cover
+    the largest expert, and the payload must hold E * N * K codes. The kernels
+    index X and Y with these values, so a bad array is a ValueError here rather
+    than an out-of-bounds access on the GPU.
+    """
     E = offsets.numel() - 1
+    if E < 1:
+        raise ValueError("offsets must hold at least two entries (one expert)")
     N, K = int(expert_shape[0]), int(expert_shape[1])
     tag = _gemm_dtype(x)
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [rows, features], got shape {tuple(x.shape)}")
     xin = _aligned(x)
     M_total = xin.shape[0]
     dev = xin.device
-    off = offsets.to(device=dev, dtype=torch.int32).contiguous()
+    host_off = offsets.detach().to("cpu", torch.int64)
+    counts = host_off[1:] - host_off[:-1]
+    if int(host_off[0]) != 0 or bool((counts < 0).any()) or int(host_off[-1]) != M_total:
+        raise ValueError(f"offsets must start at 0, be non-decreasing and end at x.shape[0] = {M_total}; "
+                         f"got {host_off.tolist()[:8]}{'...' if E > 7 else ''}")
+    largest = int(counts.max())
     if max_rows is None:
-        max_rows = int((off[1:] - off[:-1]).max().item()) if E > 0 else 0
+        max_rows = largest
+    elif int(max_rows) < largest:
+        raise ValueError(f"max_rows = {max_rows} is below the largest expert's {largest} rows")
+    if packed.numel() * 2 < E * N * K:
+        raise ValueError(f"packed holds {packed.numel() * 2} codes, {E} experts of [{N}, {K}] need {E * N * K}")
+    if absmax.numel() * blocksize < E * N * K:
+        raise ValueError(f"absmax holds {absmax.numel()} blocks, {E * N * K // blocksize} needed")
+    if not (xin.is_cuda and packed.is_cuda and absmax.is_cuda):
+        raise RuntimeError("nf4_grouped_gemm runs on the GPU kernels; x, packed and absmax must be on the GPU")
+    off = host_off.to(device=dev, dtype=torch.int32)
     out_cols = K if backward else N
     in_cols = N if backward else K
     if xin.shape[1] != in_cols:

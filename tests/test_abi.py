@@ -191,6 +191,12 @@ def test_lora_arguments_are_rejected_without_a_gpu(L):
     assert L.stm_lora_down(p, p, p, (1 << 24) + 64, 256, 16, 1.0, 1, p, 1 << 40, None) == -2
     assert L.stm_lora_workspace_bytes(64, 256, 16, 3) < 0
     assert L.stm_lora_workspace_bytes(64, 256, 40, 0) < 0
+    # widths beyond the kernels' limits are refused by the sizing call too
+    # (2^25 columns once divided by zero while planning the row blocks)
+    assert L.stm_lora_workspace_bytes(5, 1 << 25, 16, 0) == -2
+    assert L.stm_lora_workspace_bytes(5, (1 << 22) + 8, 16, 1) == -2
+    assert L.stm_lora_workspace_bytes((1 << 24) + 64, 256, 16, 2) == -2
+    assert L.stm_lora_workspace_bytes(64, 250, 16, 0) == -2
 
 
 def test_lora_workspace_sizing(L):
@@ -231,3 +237,39 @@ def test_lora_eligibility_matches_the_library_limits(L):
         # -1 here means only "workspace too small": the shape itself was accepted
         accepted = rc in (0, -1)
         assert lora_supported(rank, cols, rows) == accepted, (rank, cols, rows, rc)
+
+
+@pytest.mark.parametrize("offsets,max_rows,match", [
+    ([1, 4, 10], None, "start at 0"),           # does not start at 0
+    ([0, 6, 4, 10], None, "non-decreasing"),    # an expert with negative rows
+    ([0, 4, 12], None, "end at"),               # past the last row of x
+    ([0, 4, 8], None, "end at"),                # short of the last row
+    ([0, 4, 10], 5, "max_rows"),                # max_rows below the largest expert (6 rows)
+    ([0], None, "two entries"),                 # no expert
+])
+def test_grouped_gemm_rejects_bad_offsets_before_launch(offsets, max_rows, match):
+    """The grouped GEMM indexes X and Y with the offsets: a bad array must be a
+    ValueError on the host, never a launch (these tensors are on the CPU, so a
+    launch would touch host memory from the GPU)."""
+    import torch
+    from stratum_amd.functional import nf4_grouped_gemm
+    E = max(len(offsets) - 1, 1)
+    x = torch.zeros(10, 64, dtype=torch.bfloat16)
+    packed = torch.zeros(E * 64 * 64 // 2, dtype=torch.uint8)
+    absmax = torch.ones(E * 64, dtype=torch.float32)
+    with pytest.raises(ValueError, match=match):
+        nf4_grouped_gemm(x, packed, absmax, torch.tensor(offsets, dtype=torch.int32), (64, 64), 64,
+                         max_rows=max_rows)
+
+
+def test_grouped_gemm_rejects_a_short_payload_and_cpu_operands():
+    import torch
+    from stratum_amd.functional import nf4_grouped_gemm
+    x = torch.zeros(10, 64, dtype=torch.bfloat16)
+    off = torch.tensor([0, 4, 10], dtype=torch.int32)
+    with pytest.raises(ValueError, match="packed holds"):
+        nf4_grouped_gemm(x, torch.zeros(64 * 64 // 2, dtype=torch.uint8), torch.ones(128), off, (64, 64), 64)
+    with pytest.raises(ValueError, match="absmax holds"):
+        nf4_grouped_gemm(x, torch.zeros(64 * 64, dtype=torch.uint8), torch.ones(64), off, (64, 64), 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        nf4_grouped_gemm(x, torch.zeros(64 * 64, dtype=torch.uint8), torch.ones(128), off, (64, 64), 64)

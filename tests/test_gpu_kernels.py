@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_checks import assert_gemm_close
 from oracle import c_oracle as C
 from oracle import nf4_oracle as O
 
@@ -311,11 +312,13 @@ def test_gemm_full_lora_step_shape(cuda, dtype):
     q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
     x = seeded((M, K), 1, 1.0, dtype).to(cuda)
     y = nf4_gemm_fwd(x, q, a, (N, K), 64)
-    assert _rel(y, x.float() @ wq.t().contiguous()) <= TOL[dtype]
+    # whole matrix and every 32 x 32 fragment (persistent items past the first
+    # 256 work-groups, the XCD tile walk)
+    assert_gemm_close(y, x.float() @ wq.t().contiguous(), dtype, "forward")
     del y
     dy = seeded((M, N), 2, 1.0, dtype).to(cuda)
     dx = nf4_gemm_bwd_dx(dy, q, a, (N, K), 64)
-    assert _rel(dx, dy.float() @ wq) <= TOL[dtype]
+    assert_gemm_close(dx, dy.float() @ wq, dtype, "input gradient")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -5,7 +5,7 @@ LDS-weight kernels for some split reductions), the 128 x 256 register-weight
 tile (unsplit) or the 128 x 128 LDS-weight tile, split or not, and for a
 forward of at most 32 rows the weight-streaming small-M kernel (its reduction
 ranges summed by the split-reduce kernel, which adds bias and the LoRA term).
-STRATUM_NF4_GEMM_TILE pins the tile kind (and so skips the small-M kernel) and
+stm_nf4_gemm_set_tile pins the tile kind (and so skips the small-M kernel) and
 a call through the C ABI without a workspace pins "unsplit", so each kernel is
 reached on shapes whose rows, output columns and reduction are not multiples
 of the tile:
@@ -72,11 +72,19 @@ def bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, workspace=None
     return dx
 
 
+TILE_KIND = {None: -1, "big": 0, "small": 1, "mid": 2}
+
+
 def set_tile(monkeypatch, tile):
-    if tile is None:
-        monkeypatch.delenv("STRATUM_NF4_GEMM_TILE", raising=False)
-    else:
-        monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+    from stratum_amd import _lib
+    _lib.lib().stm_nf4_gemm_set_tile(TILE_KIND[tile])
+
+
+@pytest.fixture(autouse=True)
+def _cost_model_after_each_test():
+    yield
+    from stratum_amd import _lib
+    _lib.lib().stm_nf4_gemm_set_tile(-1)
 
 
 def variants(L, M, N, K, backward, monkeypatch, dev):
@@ -176,7 +184,7 @@ def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
     """Expert banks with empty, tiny and tile-straddling experts; 320 columns in
     the input gradient so its last tile is partly outside the matrix."""
     from stratum_amd.functional import nf4_grouped_gemm
-    monkeypatch.setenv("STRATUM_NF4_GEMM_TILE", tile)
+    set_tile(monkeypatch, tile)
     E, N, K = 6, 320, 320
     w = seeded((E, N, K), 78, 0.02, torch.float16)
     bits = w.reshape(-1, K).contiguous().view(torch.int16).numpy().view(np.uint16)
