@@ -390,7 +390,7 @@ template <typename Tr, int FA, int FB, int CX = 0, int NP = 2>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
                                                int ocol_base, int ocols, int orow_base, int orows,
                                                const uint16_t* __restrict__ bias, int lane, uint4* stage) {
-    static_assert(FB % NP == 0 && (FA == 2 || FA == 4), "64 or 128 columns per wave");
+    static_assert(FB % NP == 0 && (FA == 1 || FA == 2 || FA == 4), "32, 64 or 128 columns per wave");
     // (the register-weight kernels use FA = 2, NP = 2; the LDS-weight kernels'
     // 128 x 128 tiles store a quarter of the bytes per item and measured no gain)
     constexpr int FP = FB / NP, RP = 32 * FP, CH = 4 * FA, RPI = 64 / CH;  // rows per pass / per store
@@ -711,16 +711,16 @@ __device__ __forceinline__ void fill_lut_rw(float2* lut, int tid) {
     fill_level_table<NT, RW_LUT_COPIES>(lut, tid);
 }
 
-template <typename Tr>
+template <typename Tr, int FA = 2>
 struct RwWeights {
     struct Raw {
-        uint4 q[2];
-        float a[2];
+        uint4 q[FA];
+        float a[FA];
     };
     const uint8_t* packed;  // the group's packed weight
     const float* absmax;    // the group's absmax
-    uint32_t woff[2];       // byte offset of this lane's 16-byte run of the first step, fragment i
-    uint32_t aoff[2];       // absmax index of the start of weight row (fragment i)
+    uint32_t woff[FA];      // byte offset of this lane's 16-byte run of the first step, fragment i
+    uint32_t aoff[FA];      // absmax index of the start of weight row (fragment i)
     int64_t kbase;          // first reduction index of the work item's step range
     int bshift;
     uint32_t lut_base;     // LDS byte address of the level table
@@ -728,7 +728,7 @@ struct RwWeights {
 
     __device__ __forceinline__ void load(int64_t k0, Raw& r) const {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FA; ++i) {
             r.q[i] = *reinterpret_cast<const uint4*>(packed + (woff[i] + (uint32_t)(k0 / 2)));
             r.a[i] = absmax[aoff[i] + (uint32_t)((kbase + k0) >> bshift)];
         }
@@ -736,10 +736,10 @@ struct RwWeights {
     __device__ __forceinline__ static uint32_t word(const uint4& q, int j) {
         return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
     }
-    // table reads for sub-step j of both fragments (8 lookups)
-    __device__ __forceinline__ void issue(const Raw& r, int j, f32x2_t (&p)[2][4]) const {
+    // table reads for sub-step j of every fragment (4 lookups each)
+    __device__ __forceinline__ void issue(const Raw& r, int j, f32x2_t (&p)[FA][4]) const {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FA; ++i) {
             const uint32_t x = word(r.q[i], j);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
@@ -749,9 +749,9 @@ struct RwWeights {
             }
         }
     }
-    __device__ __forceinline__ static void finish(const Raw& r, const f32x2_t (&p)[2][4], uint4 (&out)[2]) {
+    __device__ __forceinline__ static void finish(const Raw& r, const f32x2_t (&p)[FA][4], uint4 (&out)[FA]) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FA; ++i) {
             const float a = r.a[i];
             out[i].x = Tr::pack2(opaque(p[i][0].x * a), opaque(p[i][0].y * a));
             out[i].y = Tr::pack2(opaque(p[i][1].x * a), opaque(p[i][1].y * a));
@@ -770,14 +770,14 @@ __device__ __forceinline__ void read_x(uint4 (&x)[FB], const uint4* sx, int xrow
 
 // MFMAs of one sub-step; each activation fragment is reloaded in place with
 // the fragment of sub-step jn (from buffer sx) once its two MFMAs are issued.
-template <typename Tr, int FB>
-__device__ __forceinline__ void mma_sub(f32x16_t (&acc)[2][FB], const uint4 (&w)[2], uint4 (&x)[FB],
+template <typename Tr, int FA, int FB>
+__device__ __forceinline__ void mma_sub(f32x16_t (&acc)[FA][FB], const uint4 (&w)[FA], uint4 (&x)[FB],
                                         const uint4* sx, int xrow0, int lane, int jn) {
     const int ch = 4 * (lane >> 5) + jn;
 #pragma unroll
     for (int f = 0; f < FB; ++f) {
-        acc[0][f] = mfma<Tr>(w[0], x[f], acc[0][f]);
-        acc[1][f] = mfma<Tr>(w[1], x[f], acc[1][f]);
+#pragma unroll
+        for (int i = 0; i < FA; ++i) acc[i][f] = mfma<Tr>(w[i], x[f], acc[i][f]);
         x[f] = sx[swz(xrow0 + f * 32 + (lane & 31), ch)];
     }
 }
@@ -965,7 +965,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
                    int word_next, f32x2_t (&p_next)[2][4], const typename RwWeights<Tr>::Raw& r_cur,
                    const f32x2_t (&p_cur)[2][4], uint4 (&bout)[2]) {
         ws.issue(r_next, word_next, p_next);
-        mma_sub<Tr, FB>(acc, w, x, sx, xrow0, lane, jn);
+        mma_sub<Tr, 2, FB>(acc, w, x, sx, xrow0, lane, jn);
         RwWeights<Tr>::finish(r_cur, p_cur, bout);
         rw_slot_pattern<2 * FB>();
         sched_fence();
@@ -1014,6 +1014,154 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
         store_tile_rw<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
                                  (int)N, (int)(m0 + xrow0), (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias),
                                  lane_e);
+    }
+    __syncthreads();
+    }
+}
+
+// ------------------------------ forward, register weights, two waves per SIMD
+// The 256 x 256 tile with eight waves: wave w owns the 32 output columns
+// [n0 + 32 w, n0 + 32 w + 32) over all 256 rows (8 MFMA tiles, 128
+// accumulators), so two waves share each SIMD. The dequantization per MFMA is
+// that of k_gemm_fwd_rw (each weight fragment feeds the 8 row tiles), and every
+// activation fragment now feeds one MFMA instead of two; in exchange the
+// SIMD always has a second wave to issue from while one waits on an LDS read,
+// a table lookup or the barrier (with one wave per SIMD those waits stall the
+// matrix core). Reduction order, tables and epilogue as in k_gemm_fwd_rw.
+#ifndef STM_R8_PATTERN
+#define STM_R8_PATTERN 1
+#endif
+template <int FB>
+__device__ __forceinline__ void r8_slot_pattern() {
+#if STM_R8_PATTERN
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // the four table reads ride on the first four slots
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+#pragma unroll
+    for (int k = 4; k < FB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#endif
+}
+
+template <typename Tr>
+__global__ __launch_bounds__(512, 1) void k_gemm_fwd_r8(GemmArgs g) {
+    constexpr int BM = 256, BN = 256, NT = 512, FB = BM / 32;
+    const int tid = threadIdx.x, lane0 = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    __shared__ float2 lut_all[256 * RW_LUT_COPIES];
+    __shared__ uint4 sA0[BM * 8], sA1[BM * 8];
+
+    fill_lut_rw<NT>(lut_all, tid);
+
+    const int64_t K = g.K, N = g.N;
+    const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
+    const int64_t work = tiles * g.num_groups * g.splits;
+    for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
+    const int64_t rest = w / tiles;
+    const int z = (int)(rest / g.num_groups);
+    const Group grp = group_of(g, (int)(rest % g.num_groups));
+    int64_t tm, tn;
+    tile_coords(w % tiles, ntm, ntn, tm, tn);
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= grp.rows) continue;
+
+    int s_begin, KT;
+    split_range((int)(K / BK), g.splits, z, s_begin, KT);
+    const int64_t kbase = (int64_t)s_begin * BK;
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.a) + grp.row0 * K + kbase;
+    const int lane = opaque_lane(lane0);
+
+    RwWeights<Tr, 1> ws;
+    ws.bshift = 31 - __builtin_clz(g.blocksize);
+    ws.lut_base = (uint32_t)(size_t)((const __attribute__((address_space(3))) float2*)lut_all);
+    ws.copy_off = 8u * (uint32_t)(lane & 31);
+    const int64_t col_base = n0 + wave * 32;
+    ws.packed = grp.packed;
+    ws.absmax = grp.absmax;
+    ws.kbase = kbase;
+    {
+        int64_t n = col_base + (lane & 31);
+        n = n < N ? n : N - 1;
+        ws.woff[0] = (uint32_t)(n * (K / 2) + kbase / 2 + 16 * (lane >> 5));
+        ws.aoff[0] = (uint32_t)(n * (K >> ws.bshift));
+    }
+    ActStageS<BM, 8> as;
+    as.init(X, K, m0, grp.rows, sA0, sA1, wave, lane);
+
+    f32x16_t acc[1][FB];
+    zero_acc(acc);
+
+    typename RwWeights<Tr, 1>::Raw raw0, raw1;
+    uint4 B[4][1];
+    uint4 x[FB];
+    f32x2_t pa[1][4], pb[1][4];
+
+    ws.load(0, raw0);
+    ws.load(KT > 1 ? BK : 0, raw1);
+    as.issue(0, 0);
+    wait_vmem();
+    __syncthreads();  // level table and activation tile 0 ready
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        ws.issue(raw0, j, pa);
+        RwWeights<Tr, 1>::finish(raw0, pa, B[j]);
+    }
+    ws.issue(raw0, 3, pa);
+    read_x<FB>(x, sA0, 0, lane, 0);
+    sched_fence();
+
+    auto sub = [&](const uint4 (&wf)[1], const uint4* sx, int jn, const typename RwWeights<Tr, 1>::Raw& r_next,
+                   int word_next, f32x2_t (&p_next)[1][4], const typename RwWeights<Tr, 1>::Raw& r_cur,
+                   const f32x2_t (&p_cur)[1][4], uint4 (&bout)[1]) {
+        ws.issue(r_next, word_next, p_next);
+        mma_sub<Tr, 1, FB>(acc, wf, x, sx, 0, lane, jn);
+        RwWeights<Tr, 1>::finish(r_cur, p_cur, bout);
+        r8_slot_pattern<FB>();
+        sched_fence();
+    };
+    auto step = [&](int s, const uint4* sAc, const uint4* sAn, int nbuf, typename RwWeights<Tr, 1>::Raw& rawc,
+                    const typename RwWeights<Tr, 1>::Raw& rawn) {
+        const int s1 = s + 1 < KT ? s + 1 : KT - 1;
+        const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+        as.issue((int64_t)s1 * BK, nbuf);
+        sub(B[0], sAc, 1, rawn, 0, pb, rawc, pa, B[3]);
+        ws.load((int64_t)s2 * BK, rawc);
+        sub(B[1], sAc, 2, rawn, 1, pa, rawn, pb, B[0]);
+        sub(B[2], sAc, 3, rawn, 2, pb, rawn, pa, B[1]);
+        wait_vmem();
+        __syncthreads();  // activation tile s + 1 in sAn; every wave is done reading sAc
+        sub(B[3], sAn, 0, rawn, 3, pa, rawn, pb, B[2]);
+    };
+    int s = 0;
+    for (; s + 1 < KT; s += 2) {
+        step(s, sA0, sA1, 1, raw0, raw1);
+        step(s + 1, sA1, sA0, 0, raw1, raw0);
+    }
+    if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
+
+    const int lane_e = opaque_lane(lane);
+    if (g.lora_rank > 0 && z == 0)
+        lora_term<Tr, 1, FB>(acc, reinterpret_cast<const uint16_t*>(g.lora_w), col_base, N,
+                             reinterpret_cast<const uint16_t*>(g.lora_x) + grp.row0 * g.lora_rank, m0, grp.rows,
+                             g.lora_rank, lane_e);
+    if (g.splits > 1) {
+        store_tile_f32_rw<1, FB>(acc, g.partial + (int64_t)z * g.M * N, (int)N, (int)col_base, (int)N, (int)m0,
+                                 (int)grp.rows, lane_e);
+    } else {
+        // the activation buffers stage the output: wave w takes 8 KB (128 rows
+        // x 64 bytes per pass), waves 0-3 in sA0, 4-7 in sA1
+        constexpr int RPW = 64 * FB;  // uint4 per wave
+        uint4* stage = (wave < 4 ? sA0 + wave * RPW : sA1 + (wave - 4) * RPW);
+        __syncthreads();  // every wave is done reading the activation buffers
+        store_tile_lds<Tr, 1, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
+                                     (int)N, (int)m0, (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane_e,
+                                     stage);
     }
     __syncthreads();
     }
@@ -1899,6 +2047,19 @@ int launch_bwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
     return check_launch("gemm_bwd_dx");
 }
 
+int launch_fwd_r8(const GemmArgs& g, int dtype, hipStream_t stream) {
+    const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+    if (tiles == 0) return STM_OK;
+    const int64_t work = tiles * g.num_groups * g.splits;
+    if (work > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd: grid too large");
+    dim3 grid = work_grid(work), block(512);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemm_fwd_r8<BF16>), grid, block, 0, stream, g);
+    else
+        hipLaunchKernelGGL((k_gemm_fwd_r8<F16>), grid, block, 0, stream, g);
+    return check_launch("gemm_fwd");
+}
+
 template <int BM, int WM>
 int launch_fwd_rw(const GemmArgs& g, int dtype, hipStream_t stream) {
     const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + 255) / 256);
@@ -1933,7 +2094,7 @@ constexpr int kCUs = 256;
 
 // Tile kinds: kBig = 256 x 256 (register-weight or LDS-weight kernel), kSmall =
 // 128 x 128 (LDS-weight), kMid = 128 rows x 256 columns (register-weight, unsplit).
-enum TileKind { kBig = 0, kSmall = 1, kMid = 2 };
+enum TileKind { kBig = 0, kSmall = 1, kMid = 2, kBig8 = 3 };
 
 struct Plan {
     int kind;
@@ -2036,7 +2197,7 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
 }  // namespace
 
 int set_gemm_tile(int kind) {
-    return g_tile_only.exchange(kind >= kBig && kind <= kMid ? kind : -1, std::memory_order_relaxed);
+    return g_tile_only.exchange(kind >= kBig && kind <= kBig8 ? kind : -1, std::memory_order_relaxed);
 }
 
 int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
@@ -2070,9 +2231,11 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
     int rc;
-    if (p.kind == kMid && rw_offsets_fit(g))
+    if (p.kind == kBig8 && rw_offsets_fit(g))
+        rc = launch_fwd_r8(g, dtype, stream);
+    else if (p.kind == kMid && rw_offsets_fit(g))
         rc = launch_fwd_rw<128, 1>(g, dtype, stream);
-    else if (p.kind == kBig || p.kind == kMid)
+    else if (p.kind == kBig || p.kind == kMid || p.kind == kBig8)
         rc = rw ? launch_fwd_rw<256, STM_FWD_RW_WM>(g, dtype, stream)
                 : launch_fwd_cfg<STM_FWD_BM, STM_FWD_BN, STM_FWD_WM, STM_FWD_WN>(g, dtype, stream);
     else
@@ -2089,7 +2252,7 @@ int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     int rc;
     if (p.kind == kMid && rw_offsets_fit_bwd(g))
         rc = launch_bwd_rw<128>(g, dtype, stream);
-    else if (p.kind == kBig || p.kind == kMid)
+    else if (p.kind == kBig || p.kind == kMid || p.kind == kBig8)
         rc = rw ? launch_bwd_rw<256>(g, dtype, stream)
                 : launch_bwd_cfg<STM_BWD_BM, STM_BWD_BN, STM_BWD_WM, STM_BWD_WN>(g, dtype, stream);
     else

@@ -72,7 +72,7 @@ def bwd_abi(L, stream, dy, packed, absmax, u, at, rank, N, K, bs, workspace=None
     return dx
 
 
-TILE_KIND = {None: -1, "big": 0, "small": 1, "mid": 2}
+TILE_KIND = {None: -1, "big": 0, "small": 1, "mid": 2, "big8": 3}
 
 
 def set_tile(monkeypatch, tile):
@@ -91,7 +91,7 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     """(name, tile, workspace or None) for every kernel the problem can reach;
     tile None is the library's own choice (the small-M kernel where it applies)."""
     out = []
-    for tile in (None, "big", "mid", "small"):
+    for tile in (None, "big", "big8", "mid", "small"):
         set_tile(monkeypatch, tile)
         name = tile or "auto"
         out.append((name + "-unsplit", tile, None))
@@ -178,7 +178,7 @@ def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank
         assert rel(dx, first) <= TOL[dtype] / 4, name
 
 
-@pytest.mark.parametrize("tile", ["big", "mid", "small"])
+@pytest.mark.parametrize("tile", ["big", "big8", "mid", "small"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
     """Expert banks with empty, tiny and tile-straddling experts; 320 columns in
