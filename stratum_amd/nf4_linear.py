@@ -188,3 +188,46 @@ class NF4LoRALinear(NF4Linear):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return nf4_linear(x, self.quantized, self.quant_state, self.bias, self.lora_A, self.lora_B, self.scaling)
+
+
+@torch.no_grad()
+def make_nf4_resident(module: nn.Module, device_id: int, *, lora_r: int = 0, lora_alpha: float = 16.0,
+                      lora_dtype: torch.dtype = torch.bfloat16) -> int:
+    """Keep the staged NF4 weights of *module* packed on ``cuda:<device_id>``.
+
+    Every ``nn.Linear`` inside *module* whose weight carries an NF4 payload
+    (``prepare_nf4``) is replaced by an :class:`NF4Linear` -- or, with
+    ``lora_r > 0``, an :class:`NF4LoRALinear` with fresh PEFT-style adapters --
+    that holds the payload's packed codes and absmax on the device: 0.5625
+    bytes per weight uploaded once, instead of the dequantized 2 bytes per
+    weight materialised by ``ensure_weights`` before every forward and again
+    before the recompute (``stratum/nf4_linear.py:1-8`` names this as the
+    intended use; ``stratum/pipeline.py:906`` frees after the forward). The
+    replacement keeps the payload (``.payload``) and the original bias; the
+    staging calls (``ensure_weights`` / ``free_weights``) then find nothing to
+    do for these layers. Returns the number of layers replaced.
+    """
+    from .upload import NF4_ATTR  # local: upload imports this module's package
+
+    device = torch.device("cuda", device_id)
+    replaced = 0
+    for parent in list(module.modules()):
+        for name, child in list(parent.named_children()):
+            if type(child) is not nn.Linear or not hasattr(child.weight, NF4_ATTR):
+                continue
+            payload = getattr(child.weight, NF4_ATTR)
+            if len(payload.shape) != 2:
+                continue
+            state = QuantState(absmax=payload.absmax.to(device, non_blocking=True), shape=payload.shape,
+                               code=payload.code.to(device, non_blocking=True), blocksize=payload.blocksize,
+                               quant_type=payload.quant_type, dtype=payload.dtype)
+            packed = payload.quantized.to(device, non_blocking=True)
+            bias = child.bias.detach().to(device) if child.bias is not None else None
+            if lora_r > 0:
+                new = NF4LoRALinear(packed, state, bias, r=lora_r, lora_alpha=lora_alpha, dtype=lora_dtype)
+            else:
+                new = NF4Linear(packed, state, bias)
+            new.payload = payload
+            setattr(parent, name, new)
+            replaced += 1
+    return replaced

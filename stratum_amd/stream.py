@@ -1,81 +1,187 @@
-"""Per-layer NF4 stream-in with the host-to-device copy, the dequantization and
-the layer's compute on three streams.
+"""Per-layer NF4 stream-in: host-to-device copy, dequantization and the layer's
+compute on three streams.
 
-The reference overlaps "upload + dequant of layer i+1" with "compute of layer i"
+The reference overlaps "upload + dequantize layer i+1" with "compute layer i"
 by running ``ensure_weights`` for the next layer on a side stream and fencing
-the default stream on an event (``stratum/stage.py:99-121``); upload and
-dequantization of one layer are serial on that side stream. Here the packed
-payload of layer i+1 (and further, ``lookahead``) is copied on the device's
-copy stream (``prefetch_weights``) while layer i is dequantized on a dequant
-stream (``ensure_prefetched_weights``) and layer i-1 computes on the default
-stream, so the PCIe copy, the HBM-bound dequant kernel and the compute all
-overlap. The dequantized tensors are ``record_stream``-ed on the default stream
-(the consumer), and ``free_weights`` after use returns them to the caching
-allocator safely.
+the default stream on an event (``stratum/stage.py:93-121``); the copy and the
+dequantization of one layer are serial there, and the dequantized tensors are
+made on the side stream but read on the default stream without a
+``record_stream``, so freeing them right after use lets the caching allocator
+hand their blocks to the next side-stream allocation while the reads are still
+queued.
+
+Here (``_LayerFeeder``):
+
+* the packed payloads of the next ``lookahead`` layers are copied on the
+  device's persistent copy stream (``prefetch_weights``);
+* each layer is dequantized on a dequant stream once its copy has landed
+  (event wait on the GPU, no host sync) -- FP16-staged and plain parameters
+  and buffers are brought over by the same ``ensure_weights`` call;
+* every materialised tensor is ``record_stream``-ed on the consumer stream
+  (the stream that runs the layers), and the consumer waits on a per-layer
+  event before the layer runs.
+
+``NF4LayerStream`` exposes this as an iterator; ``NF4DeviceStage`` is a
+drop-in for ``stratum.stage.DeviceStage`` (same constructor and
+``forward_range`` signature and fence protocol).
 """
 
 from __future__ import annotations
 
-from typing import Iterator, Sequence
+from contextlib import nullcontext
+from typing import Any, Iterator, Optional, Sequence
 
 import torch
+import torch.nn as nn
 
-from .upload import NF4_ATTR, ensure_prefetched_weights, free_weights, prefetch_weights
+from .upload import ensure_weights, free_weights, prefetch_weights
+
+
+class _LayerFeeder:
+    """Materialises layers of a list on one device ahead of a consumer stream."""
+
+    def __init__(self, layers: Sequence[nn.Module], device_id: int, lookahead: int,
+                 dequant_stream: "torch.cuda.Stream", consumer: "torch.cuda.Stream"):
+        if lookahead < 1:
+            raise ValueError("lookahead must be >= 1")
+        self.layers, self.device_id, self.lookahead = layers, device_id, lookahead
+        self.dequant_stream, self.consumer = dequant_stream, consumer
+        self.copies: dict = {}   # layer index -> NF4Prefetch in flight
+        self.ready: dict = {}    # layer index -> event: materialised
+
+    def _copy(self, i: int) -> None:
+        if 0 <= i < len(self.layers) and i not in self.copies and i not in self.ready:
+            self.copies[i] = prefetch_weights(self.layers[i], self.device_id)
+
+    def _materialise(self, i: int) -> None:
+        if i in self.ready or not 0 <= i < len(self.layers):
+            return
+        self._copy(i)
+        readers = [self.consumer]
+        with torch.cuda.stream(self.dequant_stream):
+            self.copies.pop(i).finalize(consumers=readers)
+            ensure_weights(self.layers[i], self.device_id, consumers=readers)
+            done = torch.cuda.Event()
+            done.record(self.dequant_stream)
+        self.ready[i] = done
+
+    def mark_ready(self, i: int, event: Optional["torch.cuda.Event"]) -> None:
+        """Layer i was materialised by the caller; *event* fences it (None: already visible)."""
+        self.copies.pop(i, None)
+        self.ready[i] = event
+
+    def before(self, i: int) -> None:
+        """Queue what layer i needs and fence the consumer on it; layer i + 1 is
+        dequantized meanwhile and the next copies are started."""
+        for j in range(i, i + 1 + self.lookahead):
+            self._copy(j)
+        self._materialise(i)
+        self._materialise(i + 1)
+        event = self.ready.pop(i)
+        if event is not None:
+            self.consumer.wait_event(event)
 
 
 class NF4LayerStream:
     """Iterate over ``layers`` with each layer's staged weights materialised on
-    ``cuda:<device_id>`` just in time.
+    ``cuda:<device_id>`` just in time::
 
         for i, layer in NF4LayerStream(stage.layers, device_id=0):
             hidden = layer(hidden)
 
-    At each yield the current stream has been fenced on layer i's dequantization;
-    when the loop body returns, the layer's dequantized weights are freed
-    (``free_after=False`` keeps them). All streams keep the default priority.
+    At each yield the current stream is fenced on layer i's materialisation.
+    When the loop body returns the layer's weights are freed (``free_after=False``
+    keeps them); that is safe with kernels still queued, since every tensor was
+    handed over to this stream. All streams keep the default priority.
     """
 
-    def __init__(self, layers: Sequence[torch.nn.Module], device_id: int = 0, *, lookahead: int = 1,
+    def __init__(self, layers: Sequence[nn.Module], device_id: int = 0, *, lookahead: int = 1,
                  free_after: bool = True):
         if lookahead < 1:
             raise ValueError("lookahead must be >= 1")
         self.layers = list(layers)
         self.device_id = device_id
-        self.device = torch.device(f"cuda:{device_id}")
         self.lookahead = lookahead
         self.free_after = free_after
-        self.dequant_stream = torch.cuda.Stream(device=self.device)
+        self.dequant_stream = torch.cuda.Stream(device=device_id)
 
     def __len__(self) -> int:
         return len(self.layers)
 
-    def _dequant(self, i: int, pending: dict) -> "torch.cuda.Event":
-        with torch.cuda.stream(self.dequant_stream):
-            ensure_prefetched_weights(self.layers[i], self.device_id, pending.pop(i))
-            ready = torch.cuda.Event()
-            ready.record(self.dequant_stream)
-        return ready
-
-    def __iter__(self) -> Iterator[tuple[int, torch.nn.Module]]:
-        n = len(self.layers)
-        if n == 0:
-            return
-        pending: dict = {}
-        ready: dict = {}
-        compute = torch.cuda.current_stream(self.device)
-        for j in range(min(n, 1 + self.lookahead)):
-            pending[j] = prefetch_weights(self.layers[j], self.device_id)
-        ready[0] = self._dequant(0, pending)
-        for i in range(n):
-            for j in range(i + 1, min(n, i + 2 + self.lookahead)):
-                if j not in pending and j not in ready:
-                    pending[j] = prefetch_weights(self.layers[j], self.device_id)
-            if i + 1 < n:  # dequantize the next layer while this one computes
-                ready[i + 1] = self._dequant(i + 1, pending)
-            compute.wait_event(ready.pop(i))
-            for p in self.layers[i].parameters():  # the compute stream is the consumer
-                if hasattr(p, NF4_ATTR) and p.data.is_cuda and p.data.numel():
-                    p.data.record_stream(compute)
-            yield i, self.layers[i]
+    def __iter__(self) -> Iterator[tuple[int, nn.Module]]:
+        feeder = _LayerFeeder(self.layers, self.device_id, self.lookahead, self.dequant_stream,
+                              torch.cuda.current_stream(self.device_id))
+        for i, layer in enumerate(self.layers):
+            feeder.before(i)
+            yield i, layer
             if self.free_after:
-                free_weights(self.layers[i])
+                free_weights(layer)
+
+
+class NF4DeviceStage(nn.Module):
+    """A contiguous slice of decoder layers on one device: drop-in for
+    ``stratum.stage.DeviceStage`` (``stratum/stage.py:14-140``).
+
+    Same constructor, ``set_timing_recorder`` and ``forward_range`` signature and
+    semantics: without ``param_stream`` the layers run as they are (the caller
+    materialised them); with it, layer weights are materialised per layer ahead
+    of the compute, ``first_layer_fence`` (if given) fences a first layer the
+    caller already uploaded, and the current stream waits on each layer's fence.
+    The materialisation itself is the three-stream one of this module:
+    ``param_stream`` is the dequant stream, payload copies run on the device's
+    copy stream ``lookahead`` layers ahead, and every tensor is handed over to
+    the consuming stream. ``free_after_use=True`` frees each layer's staged
+    weights right after its forward is queued.
+    """
+
+    def __init__(self, layers: list, device_id: int, *, lookahead: int = 1, free_after_use: bool = False):
+        super().__init__()
+        self.device_id = device_id
+        self.layers = nn.ModuleList(layers)
+        self.timing_recorder = None
+        self.layer_start = 0
+        self.lookahead = lookahead
+        self.free_after_use = free_after_use
+
+    def set_timing_recorder(self, recorder, *, layer_start: int = 0) -> None:
+        """Attach timing metadata for per-layer forward spans (``recorder.span``)."""
+        self.timing_recorder = recorder
+        self.layer_start = layer_start
+
+    def _span(self, **fields: Any):
+        if self.timing_recorder is None:
+            return nullcontext()
+        return self.timing_recorder.span("layer_forward", device_id=self.device_id, **fields)
+
+    def forward_range(self, input_data: tuple, *, local_start: int = 0, local_stop: Optional[int] = None,
+                      iter_timer=None, param_stream: Optional["torch.cuda.Stream"] = None,
+                      first_layer_fence: Optional["torch.cuda.Event"] = None) -> tuple:
+        """Run layers [local_start, local_stop) of this stage on *input_data*
+        (each layer takes and returns the tuple)."""
+        stop = len(self.layers) if local_stop is None else local_stop
+        if local_start < 0 or stop > len(self.layers) or local_start >= stop:
+            raise ValueError(f"invalid stage layer range {local_start}:{stop} for {len(self.layers)} layers")
+        run = [self.layers[i] for i in range(local_start, stop)]
+        feeder = None
+        if param_stream is not None and torch.cuda.is_available():
+            consumer = torch.cuda.current_stream(self.device_id)
+            feeder = _LayerFeeder(run, self.device_id, self.lookahead, param_stream, consumer)
+            if first_layer_fence is not None:
+                feeder.mark_ready(0, first_layer_fence)
+        for k, layer in enumerate(run):
+            if feeder is not None:
+                feeder.before(k)
+            stage_index = local_start + k
+            timed = nullcontext()
+            if iter_timer is not None and torch.cuda.is_available():
+                timed = iter_timer.time_fwd("fwd", self.layer_start + stage_index,
+                                            torch.cuda.current_stream(self.device_id))
+            with timed, self._span(stage_device=self.device_id, layer_index=self.layer_start + stage_index,
+                                   stage_layer_index=stage_index):
+                input_data = layer(input_data)
+            if self.free_after_use:
+                free_weights(layer)
+        return input_data
+
+    def forward(self, input_data: tuple) -> tuple:
+        return self.forward_range(input_data)

@@ -1,23 +1,38 @@
-"""NF4 weight staging: quantize frozen weights once, stream them to the GPU per step.
+"""NF4 weight staging: quantize frozen weights once, bring them to the GPU per step.
 
-Host-side mirror of the reference's L3 module ``stratum/upload.py`` for the NF4
-frozen-weight path, with the same names, signatures, attribute names, payload
-fields, cache format (version 1) and error behaviour, so ``DeviceStage`` /
-``StratumPipeline`` / ``ModelArch.build`` can call it unchanged. The arithmetic
-that the reference delegates to ``bitsandbytes.functional`` runs in the gfx950
-HIP library (``stratum_amd.functional``):
+Host side of the NF4 frozen-weight path with the interface of the reference's
+``stratum/upload.py`` (names, signatures, the ``NF4_ATTR`` / ``FP16_ATTR``
+attributes, ``NF4Payload`` / ``FP16StagedPayload`` fields, the version-1 cache
+files and the exception types), so ``DeviceStage`` / ``StratumPipeline`` /
+``ModelArch.build`` call it unchanged. The arithmetic the reference delegates
+to ``bitsandbytes.functional`` runs in the gfx950 HIP library
+(``stratum_amd.functional``).
 
-  prepare_nf4 / quantize_and_attach -> quantize_4bit on the GPU (payload returned to pinned host memory)
-  ensure_weights / NF4Prefetch      -> async H2D of the packed payload + dequantize_4bit kernel
+How this implementation is organised:
 
-Differences from the reference, all on the device side of the same contract:
-  * the 16-entry ``code`` table is not uploaded (the kernels carry the NF4 levels);
-  * a dequantized weight produced on a side stream is ``record_stream``-ed on the
-    device's default stream, the stream that consumes it (``stratum/stage.py:120-121``),
-    so the caching allocator cannot hand its block to the side stream again while
-    the compute that reads it is still queued;
-  * prefetches reuse one copy stream per device instead of a new stream per call;
-  * cache files are read with ``torch.load(weights_only=True)``.
+* A **staging plan** per module (``_plan``): every parameter and buffer slot of
+  the module tree as (owner module, local name, qualified name), built once
+  and cached. Slots are resolved through ``owner._parameters[name]`` on each
+  call, so a parameter replaced by ``_replace_param_data`` (or by anyone) is
+  seen; a structural change (a parameter or buffer added or removed, a child
+  module added, removed or swapped) invalidates the plan. ``ensure_weights`` /
+  ``free_weights`` / ``prefetch_weights`` therefore do not walk
+  ``named_modules`` on every call.
+* **One materialisation routine** (``_materialise``) for the three staged
+  kinds: an NF4 payload is copied host-to-device (pinned memory, asynchronous)
+  and dequantized by the GPU kernel; an FP16-staged payload is copied; a plain
+  frozen parameter on the wrong device is moved. ``ensure_weights``,
+  ``NF4Prefetch.finalize`` and ``upload_stream`` all go through it.
+* **Consumer streams.** A tensor materialised on a side stream is read by
+  other streams (the reference fences the default stream on an event,
+  ``stratum/stage.py:99-121``). Every materialised tensor -- NF4 and FP16 --
+  is ``record_stream``-ed on the consumer streams (by default the device's
+  default stream), so the caching allocator cannot hand its block to the side
+  stream again while queued consumer work still reads it (``free_weights``
+  right after a layer's forward is then safe).
+* Prefetch copies use one persistent copy stream per device; the ``code``
+  table is not uploaded (the kernels carry the NF4 levels); cache files are
+  read with ``torch.load(weights_only=True)``.
 """
 
 from __future__ import annotations
@@ -25,23 +40,26 @@ from __future__ import annotations
 import hashlib
 import re
 import time
+import weakref
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Optional, cast
+from typing import Iterable, Iterator, Optional, Sequence
 
 import torch
 
 from .functional import DEFAULT_ROUNDING, QuantState, dequantize_4bit, get_4bit_type, quantize_4bit
-from .layer_transfer import DEFAULT_CHUNK_UPLOAD_BYTES, copy_tensor_chunked
 from .utils import log_event
 
 NF4_ATTR = "roundpipe_nf4_payload"
 FP16_ATTR = "stratum_fp16_staged"
 
+_STAGEABLE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
+
+# ------------------------------------------------------------------ records
 @dataclass
 class NF4Stats:
-    """NF4 preparation statistics (``stratum/upload.py:31-45``)."""
+    """Counters of one NF4 preparation pass (``stratum/upload.py:31-45``)."""
     tensors: int = 0
     source_bytes: int = 0
     payload_bytes: int = 0
@@ -51,38 +69,24 @@ class NF4Stats:
 
     @property
     def compression(self) -> float:
-        if self.payload_bytes == 0:
-            return 0.0
-        return self.source_bytes / self.payload_bytes
+        return self.source_bytes / self.payload_bytes if self.payload_bytes else 0.0
 
+    def count(self, payload: "NF4Payload") -> None:
+        self.tensors += 1
+        self.source_bytes += payload.source_bytes
+        self.payload_bytes += payload.payload_bytes
 
-def _pin_cpu(t: torch.Tensor) -> torch.Tensor:
-    """Copy *t* to page-locked host memory (fast, asynchronous H2D)."""
-    t = t.detach().contiguous().cpu()
-    if t.is_pinned():
-        return t
-    pinned = torch.empty_like(t, device=torch.device("cpu"), pin_memory=True)
-    pinned.copy_(t)
-    return pinned
-
-
-def _payload_bytes(*tensors: torch.Tensor) -> int:
-    return sum(t.numel() * t.element_size() for t in tensors)
-
-
-def _dtype_name(dtype: torch.dtype) -> str:
-    return str(dtype).removeprefix("torch.")
-
-
-def _dtype_from_name(name: str) -> torch.dtype:
-    return cast(torch.dtype, getattr(torch, name.removeprefix("torch.")))
+    def summary(self, what: str) -> str:
+        return (f"  {what}: {self.tensors} tensors, {self.source_bytes / 2**30:.2f} GiB source -> "
+                f"{self.payload_bytes / 2**30:.2f} GiB NF4 payload ({self.compression:.2f}x; "
+                f"cache {self.cache_hits} hit / {self.cache_misses} miss / {self.cache_writes} written)")
 
 
 @dataclass
 class NF4Payload:
-    """NF4 weight payload kept in pinned host memory between steps (``stratum/upload.py:70-95``).
+    """Packed NF4 weight kept in pinned host memory (``stratum/upload.py:70-95``).
 
-    quantized: uint8 [(numel + 1) // 2, 1], two codes per byte (even element high nibble)
+    quantized: uint8 [(numel + 1) // 2, 1], two codes per byte (even element in the high nibble)
     absmax:    fp32 [ceil(numel / blocksize)]
     code:      fp32 [16], the NF4 levels
     shape:     original weight shape (3-D for stacked experts)
@@ -102,262 +106,309 @@ class NF4Payload:
 
 @dataclass
 class FP16StagedPayload:
-    """Uncompressed frozen weight kept in pinned host memory (``--no-nf4`` path)."""
+    """Uncompressed frozen weight kept in pinned host memory (the ``--no-nf4`` path)."""
     data: torch.Tensor
     shape: tuple
     dtype: torch.dtype
     source_bytes: int
 
 
-@torch.no_grad()
-def prepare_fp16_staged(module: torch.nn.Module, *, min_numel: int = 4096, verbose: bool = True) -> int:
-    """Pin frozen >=2-D params for per-step uncompressed upload (``stratum/upload.py:111-160``)."""
-    count = 0
-    for name, param in module.named_parameters():
-        if param.requires_grad:
-            continue
-        if param.numel() < min_numel:
-            continue
-        if param.ndim < 2:
-            continue
-        if hasattr(param, NF4_ATTR) or hasattr(param, FP16_ATTR):
-            continue
-        if param.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            continue
-        payload = FP16StagedPayload(
-            data=_pin_cpu(param.data),
-            shape=tuple(param.shape),
-            dtype=param.dtype,
-            source_bytes=param.numel() * param.element_size(),
-        )
-        setattr(param, FP16_ATTR, payload)
-        param.data = torch.empty(0, dtype=param.dtype, device=param.device)
-        count += 1
-    if verbose:
-        total = sum(getattr(p, FP16_ATTR).source_bytes for p in module.parameters() if hasattr(p, FP16_ATTR))
-        print(f"  fp16 staged: {count} tensors, {total / 1024**3:.2f} GiB to upload per step", flush=True)
-    return count
+def _pin_cpu(t: torch.Tensor) -> torch.Tensor:
+    """A page-locked host copy of *t* (so its host-to-device copy is asynchronous)."""
+    host = t.detach().cpu().contiguous()
+    if host.is_pinned():
+        return host
+    return host.pin_memory()
 
 
-@dataclass
-class _PrefetchEntry:
-    param: torch.nn.Parameter
-    payload: NF4Payload
-    quantized: torch.Tensor
-    absmax: torch.Tensor
-    code: torch.Tensor
-    owner: Optional[torch.nn.Module] = None
-    pname: Optional[str] = None
+def _payload_bytes(*tensors: torch.Tensor) -> int:
+    return sum(t.numel() * t.element_size() for t in tensors)
 
 
-@dataclass
-class NF4Prefetch:
-    """Pending asynchronous payload upload for one module (``stratum/upload.py:174-228``).
-
-    ``finalize()`` makes the current stream wait for the copy stream and
-    dequantizes the prefetched payloads into the parameters' data.
-    """
-    entries: list
-    device: torch.device
-    stream: Optional["torch.cuda.Stream"] = None
-    event: Optional["torch.cuda.Event"] = None
-
-    def finalize(self) -> int:
-        if not self.entries:
-            return 0
-        if self.device.type != "cuda" or not torch.cuda.is_available():
-            raise RuntimeError(f"CUDA is not available for NF4 prefetch finalize on {self.device}")
-        current = torch.cuda.current_stream(device=self.device)
-        if self.event is not None:
-            current.wait_event(self.event)
-        tensors = 0
-        with torch.cuda.device(self.device), torch.cuda.stream(current), torch.no_grad():
-            for entry in self.entries:
-                if entry.param.data.numel() > 0:
-                    if entry.param.data.device == self.device:
-                        continue
-                    _replace_param_data(entry.param,
-                                        torch.empty(0, dtype=entry.param.dtype, device=entry.param.device),
-                                        owner=entry.owner, pname=entry.pname)
-                # the uploads were made on the copy stream and are read here
-                if self.stream is not None:
-                    entry.quantized.record_stream(current)
-                    entry.absmax.record_stream(current)
-                _replace_param_data(entry.param, _dequantize_payload(entry.payload, entry.quantized, entry.absmax),
-                                    owner=entry.owner, pname=entry.pname)
-                tensors += 1
-        return tensors
-
-    def wait(self) -> int:
-        return self.finalize()
+def _dtype_name(dtype: torch.dtype) -> str:
+    return str(dtype).split(".", 1)[-1]
 
 
-def _dequantize_payload(payload: NF4Payload, q_dev: torch.Tensor, absmax_dev: torch.Tensor) -> torch.Tensor:
-    state = QuantState(absmax=absmax_dev, shape=payload.shape, code=payload.code, blocksize=payload.blocksize,
-                       quant_type=payload.quant_type, dtype=payload.dtype)
-    out = dequantize_4bit(q_dev, state).contiguous()
-    dev = out.device
-    current = torch.cuda.current_stream(dev)
-    default = torch.cuda.default_stream(dev)
-    if current != default:
-        out.record_stream(default)
-    return out
+def _dtype_from_name(name: str) -> torch.dtype:
+    dtype = getattr(torch, name.split(".", 1)[-1], None)
+    if not isinstance(dtype, torch.dtype):
+        raise ValueError(f"not a torch dtype: {name!r}")
+    return dtype
 
 
+def _eligible(param: torch.nn.Parameter, min_numel: int) -> bool:
+    """A frozen floating-point weight of >= 2 dims and >= min_numel elements: the
+    parameters both NF4 and FP16 staging take (``stratum/upload.py:111-160,305-398``)."""
+    return (not param.requires_grad and param.ndim >= 2 and param.numel() >= min_numel
+            and param.dtype in _STAGEABLE_DTYPES)
+
+
+def _staged(param: torch.nn.Parameter):
+    """The payload staged on *param* (NF4 first), or None."""
+    payload = getattr(param, NF4_ATTR, None)
+    return payload if payload is not None else getattr(param, FP16_ATTR, None)
+
+
+# ----------------------------------------------------------- staging plan
+class _Slot:
+    """One named tensor slot of a module tree (the owner held weakly)."""
+    __slots__ = ("_owner", "name", "qualname")
+
+    def __init__(self, owner: torch.nn.Module, name: str, qualname: str):
+        self._owner, self.name, self.qualname = weakref.ref(owner), name, qualname
+
+    @property
+    def owner(self) -> Optional[torch.nn.Module]:
+        return self._owner()
+
+
+class _StagePlan:
+    """Parameter and buffer slots of a module tree, with a structural fingerprint:
+    per owner, its parameter and buffer counts and the identity of its children
+    (a child swapped for another module changes it). Owners are held weakly, so
+    a cached plan never keeps a module alive."""
+
+    def __init__(self, module: torch.nn.Module):
+        owners = []
+        self.params: list = []
+        self.buffers: list = []
+        for prefix, owner in module.named_modules(remove_duplicate=False):
+            owners.append(owner)
+            dot = prefix + "." if prefix else ""
+            self.params += [_Slot(owner, n, dot + n) for n in owner._parameters]
+            self.buffers += [_Slot(owner, n, dot + n) for n in owner._buffers]
+        self.owners = [weakref.ref(o) for o in owners]
+        self.fingerprint = self._fingerprint(owners)
+
+    @staticmethod
+    def _fingerprint(owners: list) -> tuple:
+        return tuple((len(o._parameters), len(o._buffers), tuple(map(id, o._modules.values()))) for o in owners)
+
+    def valid(self) -> bool:
+        owners = [r() for r in self.owners]
+        return all(o is not None for o in owners) and self._fingerprint(owners) == self.fingerprint
+
+    def unique_params(self) -> Iterator:
+        """(slot, parameter) of every distinct parameter, first slot wins (the
+        order and de-duplication of ``named_parameters``)."""
+        seen: set = set()
+        for slot in self.params:
+            p = slot.owner._parameters.get(slot.name)
+            if p is None or id(p) in seen:
+                continue
+            seen.add(id(p))
+            yield slot, p
+
+    def unique_buffers(self) -> Iterator:
+        seen: set = set()
+        for slot in self.buffers:
+            b = slot.owner._buffers.get(slot.name)
+            if b is None or id(b) in seen:
+                continue
+            seen.add(id(b))
+            yield slot, b
+
+
+_plans: "weakref.WeakKeyDictionary[torch.nn.Module, _StagePlan]" = weakref.WeakKeyDictionary()
+
+
+def _plan(module: torch.nn.Module) -> _StagePlan:
+    """The cached staging plan of *module*, rebuilt when its structure changed."""
+    plan = _plans.get(module)
+    if plan is None or not plan.valid():
+        plan = _StagePlan(module)
+        _plans[module] = plan
+    return plan
+
+
+def _replace_param_data(param: torch.nn.Parameter, new_data: torch.Tensor, owner: Optional[torch.nn.Module] = None,
+                        pname: Optional[str] = None) -> None:
+    """Point *param* at *new_data*. Some Parameter subclasses refuse a ``.data``
+    assignment; then a plain Parameter holding *new_data* (same ``requires_grad``,
+    staged payloads carried over) is registered on *owner* under *pname* instead
+    (``stratum/upload.py:1286-1310``). Without an owner the refusal is ignored."""
+    try:
+        param.data = new_data
+        return
+    except (RuntimeError, TypeError):
+        if owner is None or pname is None:
+            return
+    replacement = torch.nn.Parameter(new_data, requires_grad=param.requires_grad)
+    for attr in (NF4_ATTR, FP16_ATTR):
+        payload = getattr(param, attr, None)
+        if payload is not None:
+            setattr(replacement, attr, payload)
+    owner.register_parameter(pname, replacement)
+
+
+def _build_param_owner_map(module: torch.nn.Module) -> dict:
+    """id(param) -> (owner module, local name), from the cached plan."""
+    return {id(p): (slot.owner, slot.name) for slot, p in _plan(module).unique_params()}
+
+
+# ----------------------------------------------------------- cache (v1)
 def _canonical_param_name(name: str) -> str:
-    """Checkpoint/cache name of a parameter inside transparent wrappers."""
+    """Cache name of a parameter: wrapper ``.module.`` segments removed."""
     return name.replace(".module.", ".")
 
 
 def _cache_path(cache_dir: Path, name: str) -> Path:
-    """``<sha1(name)[:12]>-<sanitised name[-160:]>.pt`` (``stratum/upload.py:236-240``)."""
-    name = _canonical_param_name(name)
-    safe = re.sub(r"[^A-Za-z0-9_.-]+", "_", name)[-160:]
-    digest = hashlib.sha1(name.encode("utf-8")).hexdigest()[:12]
-    return cache_dir / f"{digest}-{safe}.pt"
+    """``<sha1(name)[:12]>-<name with unsafe characters as _, last 160>.pt``
+    (the reference's file naming, ``stratum/upload.py:236-240``)."""
+    canon = _canonical_param_name(name)
+    tag = hashlib.sha1(canon.encode("utf-8")).hexdigest()[:12]
+    return Path(cache_dir) / f"{tag}-{re.sub(r'[^A-Za-z0-9_.-]+', '_', canon)[-160:]}.pt"
+
+
+def _cache_meta(shape: Sequence[int], dtype: torch.dtype, numel: int, nbytes: int, blocksize: int,
+                quant_type: str) -> dict:
+    """The metadata keys of a version-1 cache file (what a load must match)."""
+    return {"version": 1, "shape": tuple(int(s) for s in shape), "dtype": _dtype_name(dtype),
+            "blocksize": int(blocksize), "quant_type": str(quant_type), "source_numel": int(numel),
+            "source_bytes": int(nbytes)}
 
 
 def _load_payload_from_cache(path: Path, param: torch.nn.Parameter, *, blocksize: int,
                              quant_type: str) -> Optional[NF4Payload]:
-    """Read a version-1 cache file; any mismatch or unreadable file returns None."""
-    if not path.exists():
+    """A version-1 cache file whose metadata matches *param* exactly; None for a
+    missing, unreadable or mismatched file (the caller re-quantizes)."""
+    path = Path(path)
+    if not path.is_file():
         return None
+    want = _cache_meta(param.shape, param.dtype, param.numel(), param.numel() * param.element_size(), blocksize,
+                       quant_type)
     try:
         obj = torch.load(path, map_location="cpu", weights_only=True)
+        if not isinstance(obj, dict) or any(obj.get(k) != v for k, v in want.items()):
+            return None
+        tensors = [obj[k] for k in ("quantized", "absmax", "code")]
     except Exception:
         return None
-    if not isinstance(obj, dict):
+    if not all(isinstance(t, torch.Tensor) for t in tensors):
         return None
-    expected = {
-        "version": 1,
-        "shape": tuple(param.shape),
-        "dtype": _dtype_name(param.dtype),
-        "blocksize": int(blocksize),
-        "quant_type": str(quant_type),
-        "source_numel": int(param.numel()),
-        "source_bytes": int(param.numel() * param.element_size()),
-    }
-    for key, value in expected.items():
-        if obj.get(key) != value:
-            return None
-    try:
-        quantized = cast(torch.Tensor, obj["quantized"])
-        absmax = cast(torch.Tensor, obj["absmax"])
-        code = cast(torch.Tensor, obj["code"])
-    except KeyError:
-        return None
-    return NF4Payload(
-        quantized=_pin_cpu(quantized),
-        absmax=_pin_cpu(absmax),
-        code=_pin_cpu(code),
-        shape=tuple(obj["shape"]),
-        dtype=_dtype_from_name(str(obj["dtype"])),
-        blocksize=int(obj["blocksize"]),
-        quant_type=str(obj["quant_type"]),
-        source_numel=int(obj["source_numel"]),
-        source_bytes=int(obj["source_bytes"]),
-        payload_bytes=_payload_bytes(quantized, absmax, code),
-    )
+    quantized, absmax, code = (_pin_cpu(t) for t in tensors)
+    return NF4Payload(quantized=quantized, absmax=absmax, code=code, shape=want["shape"], dtype=param.dtype,
+                      blocksize=want["blocksize"], quant_type=want["quant_type"], source_numel=want["source_numel"],
+                      source_bytes=want["source_bytes"], payload_bytes=_payload_bytes(*tensors))
 
 
 def _save_payload_to_cache(path: Path, payload: NF4Payload) -> None:
-    """Atomic write (``.tmp`` + replace) of a version-1 cache file."""
+    """Write a version-1 cache file atomically (``<name>.tmp`` then rename)."""
+    path = Path(path)
     path.parent.mkdir(parents=True, exist_ok=True)
-    tmp = path.with_name(f"{path.name}.tmp")
-    torch.save({
-        "version": 1,
-        "shape": tuple(payload.shape),
-        "dtype": _dtype_name(payload.dtype),
-        "blocksize": int(payload.blocksize),
-        "quant_type": str(payload.quant_type),
-        "source_numel": int(payload.source_numel),
-        "source_bytes": int(payload.source_bytes),
-        "quantized": payload.quantized.detach().contiguous().cpu(),
-        "absmax": payload.absmax.detach().contiguous().cpu(),
-        "code": payload.code.detach().contiguous().cpu(),
-    }, tmp)
+    record = _cache_meta(payload.shape, payload.dtype, payload.source_numel, payload.source_bytes,
+                         payload.blocksize, payload.quant_type)
+    for key in ("quantized", "absmax", "code"):
+        record[key] = getattr(payload, key).detach().cpu().contiguous()
+    tmp = path.with_name(path.name + ".tmp")
+    torch.save(record, tmp)
     tmp.replace(path)
 
 
-def _nf4_eligible(param: torch.nn.Parameter, min_numel: int) -> bool:
-    return (not param.requires_grad and param.ndim >= 2 and param.numel() >= min_numel
-            and param.dtype in (torch.float16, torch.bfloat16, torch.float32))
-
-
+# ------------------------------------------------------------ preparation
 def _make_payload(data: torch.Tensor, param: torch.nn.Parameter, *, blocksize: int, quant_type: str,
                   rounding: str) -> NF4Payload:
-    orig_shape = tuple(data.shape)
-    weight = data.detach().contiguous()
-    # quantize_4bit takes a 2-D tensor; stacked expert weights [E, A, B] are
-    # flattened to [-1, B] and restored from payload.shape at dequant time
+    """Quantize *data* (the weight of *param*) on the GPU into a pinned payload.
+    Stacked expert weights [E, A, B] are quantized as their [-1, B] view and
+    keep the original shape in the payload."""
+    weight = data.detach()
     if weight.ndim > 2:
         weight = weight.reshape(-1, weight.shape[-1])
-    quantized, q_state = quantize_4bit(weight, blocksize=blocksize, compress_statistics=False,
-                                       quant_type=quant_type, rounding=rounding)
-    return NF4Payload(
-        quantized=_pin_cpu(quantized),
-        absmax=_pin_cpu(q_state.absmax),
-        code=_pin_cpu(q_state.code),
-        shape=orig_shape,
-        dtype=q_state.dtype,
-        blocksize=int(q_state.blocksize),
-        quant_type=str(q_state.quant_type),
-        source_numel=int(param.numel()),
-        source_bytes=int(param.numel() * param.element_size()),
-        payload_bytes=_payload_bytes(quantized, q_state.absmax, q_state.code),
-    )
+    packed, state = quantize_4bit(weight.contiguous(), blocksize=blocksize, compress_statistics=False,
+                                  quant_type=quant_type, rounding=rounding)
+    return NF4Payload(quantized=_pin_cpu(packed), absmax=_pin_cpu(state.absmax), code=_pin_cpu(state.code),
+                      shape=tuple(data.shape), dtype=state.dtype, blocksize=int(state.blocksize),
+                      quant_type=str(state.quant_type), source_numel=param.numel(),
+                      source_bytes=param.numel() * param.element_size(),
+                      payload_bytes=_payload_bytes(packed, state.absmax, state.code))
+
+
+def _attach(param: torch.nn.Parameter, attr: str, payload, owner=None, pname=None) -> None:
+    """Stage *payload* on *param* and drop its data (an empty tensor on the CPU
+    when the parameter lived on the meta device)."""
+    setattr(param, attr, payload)
+    home = torch.device("cpu") if param.device.type == "meta" else param.device
+    _replace_param_data(param, torch.empty(0, dtype=param.dtype, device=home), owner=owner, pname=pname)
+
+
+@torch.no_grad()
+def prepare_fp16_staged(module: torch.nn.Module, *, min_numel: int = 4096, verbose: bool = True) -> int:
+    """Move every eligible frozen weight to pinned host memory for an uncompressed
+    per-step upload (``stratum/upload.py:111-160``); returns how many were staged."""
+    staged = 0
+    for slot, p in _plan(module).unique_params():
+        if not _eligible(p, min_numel) or _staged(p) is not None:
+            continue
+        payload = FP16StagedPayload(data=_pin_cpu(p.data), shape=tuple(p.shape), dtype=p.dtype,
+                                    source_bytes=p.numel() * p.element_size())
+        _attach(p, FP16_ATTR, payload, slot.owner, slot.name)
+        staged += 1
+    if verbose:
+        total = sum(getattr(p, FP16_ATTR).source_bytes for _, p in _plan(module).unique_params()
+                    if hasattr(p, FP16_ATTR))
+        print(f"  fp16 staged: {staged} new tensors, {total / 2**30:.2f} GiB uploaded per step", flush=True)
+    return staged
 
 
 @torch.no_grad()
 def prepare_nf4(module: torch.nn.Module, *, min_numel: int = 4096, cache_dir: Optional[Path | str] = None,
                 verbose: bool = True, blocksize: int = 64, quant_type: str = "nf4",
                 rounding: str = DEFAULT_ROUNDING) -> NF4Stats:
-    """Quantize frozen >=2-D weights to NF4, attach the payload, drop the originals
-    (``stratum/upload.py:305-398``). The weight is quantized by the GPU kernel and
-    the payload comes back to pinned host memory; ``param.data`` becomes empty.
-    """
+    """Quantize every eligible frozen weight to NF4 (GPU kernel), keep the payload in
+    pinned host memory and empty the parameter (``stratum/upload.py:305-398``).
+    A parameter that already carries a payload is counted, not re-quantized; with
+    *cache_dir*, matching version-1 cache files are used and misses are written."""
     stats = NF4Stats()
-    for name, param in module.named_parameters():
-        if param.requires_grad:
+    for slot, p in _plan(module).unique_params():
+        if not _eligible(p, min_numel):
             continue
-        if param.ndim < 2:
-            continue
-        if param.numel() < min_numel:
-            continue
-        if param.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            continue
-        if hasattr(param, NF4_ATTR):
-            payload = cast(NF4Payload, getattr(param, NF4_ATTR))
-            stats.tensors += 1
-            stats.source_bytes += payload.source_bytes
-            stats.payload_bytes += payload.payload_bytes
-            continue
-
-        cache_path = _cache_path(Path(cache_dir), name) if cache_dir else None
-        payload = (_load_payload_from_cache(cache_path, param, blocksize=blocksize, quant_type=quant_type)
-                   if cache_path is not None else None)
-        if payload is not None:
-            stats.cache_hits += 1
+        payload = getattr(p, NF4_ATTR, None)
         if payload is None:
-            if cache_path is not None:
-                stats.cache_misses += 1
-            payload = _make_payload(param.data, param, blocksize=blocksize, quant_type=quant_type, rounding=rounding)
-            if cache_path:
-                _save_payload_to_cache(cache_path, payload)
-                stats.cache_writes += 1
-
-        setattr(param, NF4_ATTR, payload)
-        param.data = torch.empty(0, dtype=payload.dtype, device=param.device)
-        stats.tensors += 1
-        stats.source_bytes += payload.source_bytes
-        stats.payload_bytes += payload.payload_bytes
-
+            path = _cache_path(Path(cache_dir), slot.qualname) if cache_dir else None
+            payload = _load_payload_from_cache(path, p, blocksize=blocksize, quant_type=quant_type) if path else None
+            if payload is not None:
+                stats.cache_hits += 1
+            else:
+                payload = _make_payload(p.data, p, blocksize=blocksize, quant_type=quant_type, rounding=rounding)
+                if path is not None:
+                    stats.cache_misses += 1
+                    _save_payload_to_cache(path, payload)
+                    stats.cache_writes += 1
+            _attach(p, NF4_ATTR, payload, slot.owner, slot.name)
+        stats.count(payload)
     if verbose:
-        print(f"  nf4 total: {stats.tensors} tensors, "
-              f"{stats.source_bytes / 1024**3:.2f} GiB -> {stats.payload_bytes / 1024**3:.2f} GiB payload "
-              f"(compression {stats.compression:.2f}x, "
-              f"cache hits={stats.cache_hits} misses={stats.cache_misses} writes={stats.cache_writes})",
-              flush=True)
+        print(stats.summary("nf4 prepared"), flush=True)
+    return stats
+
+
+@torch.no_grad()
+def prepare_nf4_from_cache(module: torch.nn.Module, cache_dir: str | Path | None, *, min_numel: int = 4096,
+                           blocksize: int = 64, quant_type: str = "nf4", verbose: bool = True) -> Optional[NF4Stats]:
+    """Attach cached payloads to every eligible parameter (meta parameters too)
+    without reading any weight; None as soon as one file is missing or stale, so
+    the caller can fall back to a full load (``stratum/upload.py:1207-1283``)."""
+    if cache_dir is None:
+        return None
+    stats = NF4Stats()
+    pending = []
+    for slot, p in _plan(module).unique_params():
+        if not _eligible(p, min_numel):
+            continue
+        payload = getattr(p, NF4_ATTR, None)
+        if payload is None:
+            payload = _load_payload_from_cache(_cache_path(Path(cache_dir), slot.qualname), p, blocksize=blocksize,
+                                               quant_type=quant_type)
+            if payload is None:
+                if verbose:
+                    print(f"  nf4 cache: no usable file for {slot.qualname}", flush=True)
+                return None
+            stats.cache_hits += 1
+            pending.append((slot, p, payload))
+        stats.count(payload)
+    for slot, p, payload in pending:  # attach only once every file was found
+        _attach(p, NF4_ATTR, payload, slot.owner, slot.name)
+    if verbose:
+        print(stats.summary("nf4 from cache"), flush=True)
     return stats
 
 
@@ -366,326 +417,287 @@ def quantize_and_attach(name: str, param: torch.nn.Parameter, data: torch.Tensor
                         cache_dir: Optional[Path | str] = None, blocksize: int = 64, quant_type: str = "nf4",
                         owner: Optional[torch.nn.Module] = None, pname: Optional[str] = None,
                         rounding: str = DEFAULT_ROUNDING) -> NF4Payload:
-    """Quantize one freshly loaded tensor and attach it to *param* -- the per-tensor
-    step of the streaming low-RSS build (``stratum/upload.py:718-754``)."""
+    """Quantize one freshly loaded tensor for *param* and stage it (the per-tensor
+    step of a streaming build, ``stratum/upload.py:718-754``)."""
     payload = _make_payload(data, param, blocksize=blocksize, quant_type=quant_type, rounding=rounding)
     if cache_dir:
+        stats.cache_misses += 1
         _save_payload_to_cache(_cache_path(Path(cache_dir), name), payload)
         stats.cache_writes += 1
-        stats.cache_misses += 1
-    setattr(param, NF4_ATTR, payload)
-    _replace_param_data(param, torch.empty(0, dtype=payload.dtype, device="cpu"), owner=owner, pname=pname)
-    stats.tensors += 1
-    stats.source_bytes += payload.source_bytes
-    stats.payload_bytes += payload.payload_bytes
+    _attach(param, NF4_ATTR, payload, owner, pname)
+    stats.count(payload)
     return payload
 
 
 @torch.no_grad()
 def estimate_module_upload_gib(module: torch.nn.Module) -> float:
-    """GPU footprint of a module with NF4 params counted at their dequantized size."""
+    """Device footprint of *module* (GB, 10^9) with staged weights at their
+    materialised size; a shared parameter counts once."""
     total = 0
-    seen: set = set()
-    for param in module.parameters():
-        if id(param) in seen:
-            continue
-        seen.add(id(param))
-        payload = getattr(param, NF4_ATTR, None)
-        if payload is not None:
-            total += payload.source_bytes
-        else:
-            total += param.numel() * param.element_size()
-        if param.grad is not None:
-            total += param.grad.numel() * param.grad.element_size()
-    for buf in module.buffers():
-        total += buf.numel() * buf.element_size()
-    return total / 10**9
+    for _, p in _plan(module).unique_params():
+        payload = _staged(p)
+        total += payload.source_bytes if payload is not None else p.numel() * p.element_size()
+        if p.grad is not None:
+            total += p.grad.numel() * p.grad.element_size()
+    total += sum(b.numel() * b.element_size() for _, b in _plan(module).unique_buffers())
+    return total / 1e9
 
 
-@torch.no_grad()
-def upload_stream(module: torch.nn.Module, device_id: int, *, verbose: bool = True) -> int:
-    """Upload every param/buffer of *module* once (synchronous copies); NF4 params
-    are uploaded packed and dequantized on the GPU (``stratum/upload.py:907-966``)."""
-    device = torch.device(f"cuda:{device_id}")
-    tensors = 0
-    t0 = time.time()
-    for name, param in module.named_parameters():
-        if param.data.device == device:
-            continue
-        payload = getattr(param, NF4_ATTR, None)
-        if payload is not None:
-            q_gpu = payload.quantized.to(device, non_blocking=False)
-            a_gpu = payload.absmax.to(device, non_blocking=False)
-            with torch.cuda.device(device):
-                param.data = _dequantize_payload(payload, q_gpu, a_gpu)
-            tensors += 1
-            if verbose:
-                mib = payload.quantized.numel() * payload.quantized.element_size() / 1024**2
-                print(f"  stream {name}: nf4 {list(payload.shape)} -> {mib:.1f} MiB on GPU", flush=True)
-        else:
-            param.data = param.data.to(device, non_blocking=False)
-            tensors += 1
-    for buf in module.buffers():
-        if buf.data.device == device:
-            continue
-        buf.data = buf.data.to(device, non_blocking=False)
-    dt = time.time() - t0
-    log_event("upload_stream", device=device_id, tensors=tensors, seconds=round(dt, 1))
-    if verbose:
-        print(f"  device {device_id}: {tensors} tensors in {dt:.1f}s", flush=True)
-    return tensors
+# -------------------------------------------------------- materialisation
+def _cuda(device_id) -> torch.device:
+    dev = torch.device("cuda", device_id) if isinstance(device_id, int) else torch.device(device_id)
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        raise RuntimeError(f"no GPU available to materialise staged weights on {dev}")
+    return dev
 
 
-@torch.no_grad()
-def ensure_weights(module: torch.nn.Module, device_id: int) -> int:
-    """Materialise every staged parameter of *module* on ``cuda:<device_id>``
-    (``stratum/upload.py:969-1069``): FP16-staged params are copied in chunks, NF4
-    payloads are uploaded packed (asynchronously, from pinned memory) and
-    dequantized by the GPU kernel, other params/buffers are moved if needed.
-    Runs on the current stream. Returns the number of tensors touched.
-    """
-    device = torch.device(f"cuda:{device_id}")
-    tensors = 0
-    owner_map = _build_param_owner_map(module)
-    for name, param in module.named_parameters():
-        fp16_payload = getattr(param, FP16_ATTR, None)
-        if fp16_payload is not None:
-            if param.data.numel() > 0:
-                if param.data.device == device:
-                    continue
-                # shared staged param reached from another device: re-upload here
-                param.data = torch.empty(0, dtype=param.dtype, device=param.device)
-            dst = torch.empty(fp16_payload.shape, dtype=fp16_payload.dtype, device=device)
-            copy_tensor_chunked(fp16_payload.data, dst, chunk_bytes=DEFAULT_CHUNK_UPLOAD_BYTES, non_blocking=True)
-            param.data = dst
-            tensors += 1
-            continue
-        payload = getattr(param, NF4_ATTR, None)
-        if payload is None:
-            if param.data.numel() > 0 and param.data.device != device:
-                if param.requires_grad:
-                    raise RuntimeError(
-                        f"trainable shared parameter {name!r} is on {param.data.device}, "
-                        f"but module is running on {device}; Stratum cannot safely move "
-                        "trainable parameters between stages")
-                param.data = param.data.to(device, non_blocking=True)
-                tensors += 1
-            continue
-        if param.data.numel() > 0:
-            if param.data.device == device:
-                continue  # already materialised on the target device
-            # shared frozen weight used on another device: re-materialise from the payload
-            target = "cpu" if param.device.type == "meta" else param.device
-            owner, pname = owner_map.get(id(param), (None, None))
-            _replace_param_data(param, torch.empty(0, dtype=param.dtype, device=target), owner=owner, pname=pname)
-        q_gpu = payload.quantized.to(device, non_blocking=True)
-        a_gpu = payload.absmax.to(device, non_blocking=True)
-        owner, pname = owner_map.get(id(param), (None, None))
+def _consumers(device: torch.device, consumers: Optional[Iterable]) -> list:
+    """Streams that will read tensors materialised now: the given ones, else the
+    device's default stream; the current stream itself needs no record."""
+    current = torch.cuda.current_stream(device)
+    wanted = list(consumers) if consumers is not None else [torch.cuda.default_stream(device)]
+    return [s for s in wanted if s != current]
+
+
+def _hand_over(t: torch.Tensor, consumers: list) -> torch.Tensor:
+    for s in consumers:
+        t.record_stream(s)
+    return t
+
+
+def _dequantize_payload(payload: NF4Payload, q_dev: torch.Tensor, absmax_dev: torch.Tensor,
+                        consumers: Optional[Iterable] = None) -> torch.Tensor:
+    """The weight of *payload* from its packed bytes already on the device
+    (current stream), handed over to the consumer streams."""
+    state = QuantState(absmax=absmax_dev, shape=payload.shape, code=payload.code, blocksize=payload.blocksize,
+                       quant_type=payload.quant_type, dtype=payload.dtype)
+    w = dequantize_4bit(q_dev, state)
+    return _hand_over(w, _consumers(w.device, consumers))
+
+
+def _upload_nf4(payload: NF4Payload, device: torch.device):
+    """Packed codes and absmax of *payload* on *device* (asynchronous from pinned
+    memory, on the current stream)."""
+    return (payload.quantized.to(device, non_blocking=True), payload.absmax.to(device, non_blocking=True))
+
+
+def _needs(p: torch.nn.Parameter, device: torch.device) -> bool:
+    """A staged parameter has to be (re)materialised on *device*: it is empty, or
+    materialised on another device (a weight shared by stages on two GPUs)."""
+    return p.data.numel() == 0 or p.data.device != device
+
+
+def _materialise(slot: _Slot, p: torch.nn.Parameter, device: torch.device, consumers: list,
+                 prefetched=None) -> int:
+    """Bring one parameter to *device* on the current stream; returns 1 if a
+    tensor was placed. NF4: H2D of the packed payload (or the prefetched copy)
+    and dequantize; FP16-staged: H2D copy; other frozen parameters are moved,
+    trainable ones on another device are an error (Stratum never moves them)."""
+    nf4 = getattr(p, NF4_ATTR, None)
+    fp16 = getattr(p, FP16_ATTR, None) if nf4 is None else None
+    if nf4 is None and fp16 is None:
+        if p.data.numel() == 0 or p.data.device == device:
+            return 0
+        if p.requires_grad:
+            raise RuntimeError(f"parameter {slot.qualname!r} is trainable and lives on {p.data.device}; "
+                               f"a stage on {device} cannot take it over")
+        p.data = p.data.to(device, non_blocking=True)
+        return 1
+    if not _needs(p, device):
+        return 0
+    if nf4 is not None:
+        q_dev, a_dev = prefetched if prefetched is not None else _upload_nf4(nf4, device)
         with torch.cuda.device(device):
-            weight = _dequantize_payload(payload, q_gpu, a_gpu)
-        _replace_param_data(param, weight, owner=owner, pname=pname)
-        tensors += 1
-    for buf in module.buffers():
-        replaced = False
-        if buf.device.type == "meta":
+            w = _dequantize_payload(nf4, q_dev, a_dev, consumers)
+    else:
+        w = torch.empty(fp16.shape, dtype=fp16.dtype, device=device)
+        w.copy_(fp16.data, non_blocking=True)
+        _hand_over(w, consumers)
+    _replace_param_data(p, w, owner=slot.owner, pname=slot.name)
+    return 1
+
+
+def _materialise_buffers(plan: _StagePlan, device: torch.device) -> int:
+    """Move buffers to *device*; a meta buffer becomes an (uninitialised) tensor
+    allocated there directly, registered on its owner when ``.data`` is refused."""
+    moved = 0
+    for slot, b in plan.unique_buffers():
+        if b.device == device:
+            continue
+        if b.device.type == "meta":
+            fresh = torch.empty(b.shape, dtype=b.dtype, device=device)
             try:
-                buf.data = torch.empty(buf.shape, dtype=buf.dtype, device="cpu")
+                b.data = fresh
             except (RuntimeError, TypeError):
-                for _m_name, sub in module.named_modules():
-                    for b_name, b in sub.named_buffers(recurse=False):
-                        if b is buf:
-                            new_b = torch.empty(buf.shape, dtype=buf.dtype, device="cpu")
-                            sub.register_buffer(b_name, new_b)
-                            buf = new_b
-                            replaced = True
-                            break
-                    else:
-                        continue
-                    break
-        if replaced:
-            buf.data = buf.data.to(device, non_blocking=True)
-            tensors += 1
-        elif buf.data.device != device:
-            buf.data = buf.data.to(device, non_blocking=True)
-            tensors += 1
-    return tensors
-
-
-_copy_streams: dict = {}
-
-
-def _copy_stream(device: torch.device) -> "torch.cuda.Stream":
-    """One persistent H2D copy stream per device (default priority)."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
-    s = _copy_streams.get(key)
-    if s is None:
-        s = torch.cuda.Stream(device=device)
-        _copy_streams[key] = s
-    return s
+                persistent = slot.name not in slot.owner._non_persistent_buffers_set
+                slot.owner.register_buffer(slot.name, fresh, persistent=persistent)
+        else:
+            b.data = b.data.to(device, non_blocking=True)
+        moved += 1
+    return moved
 
 
 @torch.no_grad()
-def prefetch_weights(module: torch.nn.Module, device_id: int) -> NF4Prefetch:
-    """Start the asynchronous H2D copies of the packed payloads of *module*'s empty
-    NF4 params on the device's copy stream (``stratum/upload.py:1072-1125``).
-    Parameter data is not touched until ``NF4Prefetch.finalize()``."""
-    device = torch.device(f"cuda:{device_id}")
-    owner_map = _build_param_owner_map(module)
-    entries: list = []
-    for name, param in module.named_parameters():
-        payload = getattr(param, NF4_ATTR, None)
-        if payload is None:
-            continue
-        if param.data.numel() > 0 and param.data.device == device:
-            continue
-        owner, pname = owner_map.get(id(param), (None, None))
-        p = cast(NF4Payload, payload)
-        entries.append(_PrefetchEntry(param=param, payload=p, quantized=p.quantized, absmax=p.absmax, code=p.code,
-                                      owner=owner, pname=pname))
-    if not entries:
-        return NF4Prefetch([], device)
-    if device.type != "cuda" or not torch.cuda.is_available():
-        raise RuntimeError(f"CUDA is not available for NF4 prefetch to {device}")
-    stream = _copy_stream(device)
-    prefetched: list = []
-    with torch.cuda.device(device), torch.cuda.stream(stream):
-        for e in entries:
-            prefetched.append(_PrefetchEntry(
-                param=e.param, payload=e.payload,
-                quantized=e.quantized.to(device, non_blocking=True),
-                absmax=e.absmax.to(device, non_blocking=True),
-                code=e.code, owner=e.owner, pname=e.pname))
-        event = torch.cuda.Event()
-        stream.record_event(event)
-    return NF4Prefetch(prefetched, device=device, stream=stream, event=event)
-
-
-@torch.no_grad()
-def ensure_prefetched_weights(module: torch.nn.Module, device_id: int, prefetch: Optional[NF4Prefetch]) -> int:
-    """Finalize a matching prefetch, then run the regular ensure for the rest."""
-    if prefetch is None:
-        return ensure_weights(module, device_id)
-    if prefetch.device != torch.device(f"cuda:{device_id}"):
-        raise ValueError(f"prefetch device {prefetch.device} does not match cuda:{device_id}")
-    return prefetch.finalize() + ensure_weights(module, device_id)
+def ensure_weights(module: torch.nn.Module, device_id: int, *, consumers: Optional[Sequence] = None) -> int:
+    """Materialise every staged parameter and every buffer of *module* on
+    ``cuda:<device_id>`` (``stratum/upload.py:969-1069``); the opposite of
+    ``free_weights``. GPU work is queued on the current stream; the tensors are
+    handed over to *consumers* (default: the device's default stream, the
+    stream the reference fences on the upload). Returns the number of tensors
+    placed."""
+    device = _cuda(device_id)
+    plan = _plan(module)
+    readers = _consumers(device, consumers)
+    placed = sum(_materialise(slot, p, device, readers) for slot, p in plan.unique_params())
+    return placed + _materialise_buffers(plan, device)
 
 
 @torch.no_grad()
 def free_weights(module: torch.nn.Module) -> int:
-    """Drop the materialised data of staged params (payload kept). Returns the count."""
-    tensors = 0
-    for _name, param in module.named_parameters():
-        if not hasattr(param, NF4_ATTR) and not hasattr(param, FP16_ATTR):
-            continue
-        if param.data.numel() == 0:
-            continue
-        param.data = torch.empty(0, dtype=param.dtype, device=param.device)
-        tensors += 1
-    return tensors
+    """Drop the device data of every staged parameter of *module* (the payloads
+    stay); returns how many were dropped (``stratum/upload.py:1144-1159``)."""
+    dropped = 0
+    for _, p in _plan(module).unique_params():
+        if p.data.numel() and _staged(p) is not None:
+            p.data = torch.empty(0, dtype=p.dtype, device=p.device)
+            dropped += 1
+    return dropped
 
 
 @torch.no_grad()
+def upload_stream(module: torch.nn.Module, device_id: int, *, verbose: bool = True) -> int:
+    """Materialise *module* on ``cuda:<device_id>`` once and wait for it: staged
+    weights through ``ensure_weights``' path, everything else moved
+    (``stratum/upload.py:907-966``)."""
+    t0 = time.time()
+    device = _cuda(device_id)
+    placed = ensure_weights(module, device_id)
+    torch.cuda.current_stream(device).synchronize()
+    seconds = time.time() - t0
+    log_event("upload_stream", device=device_id, tensors=placed, seconds=round(seconds, 1))
+    if verbose:
+        print(f"  device {device_id}: {placed} tensors in {seconds:.1f}s", flush=True)
+    return placed
+
+
+# ----------------------------------------------------------------- prefetch
+_copy_streams: dict = {}
+
+
+def _copy_stream(device: torch.device) -> "torch.cuda.Stream":
+    """The persistent host-to-device copy stream of *device* (default priority)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _copy_streams.get(index)
+    if stream is None:
+        stream = _copy_streams[index] = torch.cuda.Stream(device=index)
+    return stream
+
+
+@dataclass
+class _PrefetchEntry:
+    slot: _Slot
+    param: torch.nn.Parameter
+    payload: NF4Payload
+    quantized: torch.Tensor  # device copy (copy stream)
+    absmax: torch.Tensor
+
+
+@dataclass
+class NF4Prefetch:
+    """Packed payloads of one module in flight to a device (``stratum/upload.py:174-228``).
+
+    ``finalize()`` (alias ``wait()``) makes the current stream wait for the
+    copies and dequantizes them into the parameters; an empty prefetch is a
+    no-op that needs no GPU.
+    """
+    entries: list
+    device: torch.device
+    stream: Optional["torch.cuda.Stream"] = None
+    event: Optional["torch.cuda.Event"] = None
+
+    @torch.no_grad()
+    def finalize(self, *, consumers: Optional[Sequence] = None) -> int:
+        if not self.entries:
+            return 0
+        device = _cuda(self.device)
+        current = torch.cuda.current_stream(device)
+        if self.event is not None:
+            current.wait_event(self.event)
+        readers = _consumers(device, consumers)
+        placed = 0
+        for e in self.entries:
+            if not _needs(e.param, device):
+                continue  # materialised meanwhile (e.g. by an ensure_weights)
+            e.quantized.record_stream(current)  # allocated on the copy stream, read here
+            e.absmax.record_stream(current)
+            placed += _materialise(e.slot, e.param, device, readers, prefetched=(e.quantized, e.absmax))
+        self.entries = []
+        return placed
+
+    def wait(self) -> int:
+        return self.finalize()
+
+
+@torch.no_grad()
+def prefetch_weights(module: torch.nn.Module, device_id: int) -> NF4Prefetch:
+    """Start the host-to-device copies of the packed payloads of *module*'s NF4
+    parameters that are not materialised on ``cuda:<device_id>``, on the device's
+    copy stream; parameters are not touched until ``finalize()``
+    (``stratum/upload.py:1072-1125``)."""
+    device = torch.device("cuda", device_id)
+    todo = [(slot, p, getattr(p, NF4_ATTR)) for slot, p in _plan(module).unique_params()
+            if hasattr(p, NF4_ATTR) and _needs(p, device)]
+    if not todo:
+        return NF4Prefetch([], device)
+    device = _cuda(device)
+    stream = _copy_stream(device)
+    with torch.cuda.device(device), torch.cuda.stream(stream):
+        entries = [_PrefetchEntry(slot, p, payload, *_upload_nf4(payload, device)) for slot, p, payload in todo]
+        done = torch.cuda.Event()
+        done.record(stream)
+    return NF4Prefetch(entries, device=device, stream=stream, event=done)
+
+
+@torch.no_grad()
+def ensure_prefetched_weights(module: torch.nn.Module, device_id: int, prefetch: Optional[NF4Prefetch]) -> int:
+    """Finalize *prefetch* (it must target ``cuda:<device_id>``), then run
+    ``ensure_weights`` for what a prefetch does not carry (FP16-staged and plain
+    parameters, buffers)."""
+    if prefetch is None:
+        return ensure_weights(module, device_id)
+    if prefetch.device != torch.device("cuda", device_id):
+        raise ValueError(f"prefetch targets {prefetch.device}, not cuda:{device_id}")
+    return prefetch.finalize() + ensure_weights(module, device_id)
+
+
+# ------------------------------------------------------- buffer snapshots
+@torch.no_grad()
 def snapshot_module_buffers(module: torch.nn.Module) -> dict:
-    """CPU clones of all non-empty buffers, for restoring before a recompute."""
-    snap: dict = {}
-    for name, buf in module.named_buffers():
-        if buf.numel() > 0:
-            snap[name] = buf.detach().to("cpu", non_blocking=False).clone()
-    return snap
+    """Host clones of the non-empty buffers of *module*, by qualified name (taken
+    before a forward whose recompute must see the same buffer state)."""
+    return {name: b.detach().to("cpu", copy=True) for name, b in module.named_buffers() if b.numel()}
 
 
 @torch.no_grad()
 def restore_module_buffers(module: torch.nn.Module, snapshot: dict) -> int:
-    """Copy a snapshot back into the module's buffers. Returns the number restored."""
+    """Copy a snapshot back into *module*'s buffers; returns how many were restored."""
     if not snapshot:
         return 0
-    buf_map = dict(module.named_buffers())
+    current = dict(module.named_buffers())
     restored = 0
-    for name, cpu_clone in snapshot.items():
-        buf = buf_map.get(name)
-        if buf is None:
-            continue
-        buf.data.copy_(cpu_clone.to(buf.device, non_blocking=False))
-        restored += 1
+    for name, saved in snapshot.items():
+        b = current.get(name)
+        if b is not None:
+            b.copy_(saved.to(b.device))
+            restored += 1
     return restored
 
 
-@torch.no_grad()
-def prepare_nf4_from_cache(module: torch.nn.Module, cache_dir: str | Path | None, *, min_numel: int = 4096,
-                           blocksize: int = 64, quant_type: str = "nf4", verbose: bool = True) -> Optional[NF4Stats]:
-    """Attach cached payloads to every eligible param (meta params allowed); None on
-    the first miss so the caller can fall back (``stratum/upload.py:1207-1283``)."""
-    if cache_dir is None:
-        return None
-    cache_root = Path(cache_dir)
-    stats = NF4Stats()
-    owner_map = _build_param_owner_map(module)
-    for name, param in module.named_parameters():
-        if param.requires_grad:
-            continue
-        if param.ndim < 2:
-            continue
-        if param.numel() < min_numel:
-            continue
-        if param.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            continue
-        if hasattr(param, NF4_ATTR):
-            payload = cast(NF4Payload, getattr(param, NF4_ATTR))
-            stats.tensors += 1
-            stats.source_bytes += payload.source_bytes
-            stats.payload_bytes += payload.payload_bytes
-            continue
-        payload = _load_payload_from_cache(_cache_path(cache_root, name), param, blocksize=blocksize,
-                                           quant_type=quant_type)
-        if payload is None:
-            if verbose:
-                print(f"  nf4 cache miss: {name} -- requires FP16 load", flush=True)
-            return None
-        stats.cache_hits += 1
-        setattr(param, NF4_ATTR, payload)
-        owner, pname = owner_map.get(id(param), (None, None))
-        _replace_param_data(param, torch.empty(0, dtype=payload.dtype, device="cpu"), owner=owner, pname=pname)
-        stats.tensors += 1
-        stats.source_bytes += payload.source_bytes
-        stats.payload_bytes += payload.payload_bytes
-    if verbose:
-        print(f"  nf4 from cache: {stats.tensors} tensors, {stats.source_bytes / 1024**3:.2f} GiB source -> "
-              f"{stats.payload_bytes / 1024**3:.2f} GiB payload (cache hits={stats.cache_hits})", flush=True)
-    return stats
-
-
-def _replace_param_data(param: torch.nn.Parameter, new_data: torch.Tensor, owner: Optional[torch.nn.Module] = None,
-                        pname: Optional[str] = None) -> None:
-    """``param.data = new_data``; when a Parameter subclass refuses, register a new
-    Parameter (payload attributes carried over) on *owner* (``stratum/upload.py:1286-1310``)."""
-    try:
-        param.data = new_data
-        return
-    except (RuntimeError, TypeError):
-        pass
-    if owner is not None and pname is not None:
-        new_param = torch.nn.Parameter(new_data, requires_grad=param.requires_grad)
-        for attr in (NF4_ATTR, FP16_ATTR):
-            if hasattr(param, attr):
-                setattr(new_param, attr, getattr(param, attr))
-        owner.register_parameter(pname, new_param)
-
-
-def _build_param_owner_map(module: torch.nn.Module) -> dict:
-    """id(param) -> (owner module, local name)."""
-    pmap: dict = {}
-    for _m_name, sub in module.named_modules():
-        for p_name, p in sub.named_parameters(recurse=False):
-            pmap[id(p)] = (sub, p_name)
-    return pmap
-
-
 def nf4_code_table(device=None) -> torch.Tensor:
-    """The fp32 [16] NF4 level table stored in ``NF4Payload.code``."""
+    """The fp32 [16] NF4 level table kept in ``NF4Payload.code``."""
     return get_4bit_type("nf4", device=device)
 
 
-# Checkpoint loaders (stratum/upload.py:425-904,1325-1440) live in .checkpoint;
-# imported last because they use this module's helpers.
-from .checkpoint import (_build_ckpt_key_fn, _try_load_fused_experts, load_module_fp16_from_checkpoint,  # noqa: E402
-                         populate_from_hf_checkpoint, stream_load_and_quantize_module)
+# The checkpoint build (stream_load_and_quantize_module) lives in .checkpoint;
+# imported last because it uses this module's helpers.
+from .checkpoint import stream_load_and_quantize_module  # noqa: E402

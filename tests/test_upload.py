@@ -181,20 +181,6 @@ def test_free_keeps_the_host_copy_of_fp16_staged():
     assert free_weights(m) == 1 and m.weight.numel() == 0 and pay.data.numel() == 64
 
 
-def test_copy_tensor_chunked_splits_and_checks():
-    from stratum_amd.layer_transfer import copy_tensor_chunked
-    src = torch.arange(1000, dtype=torch.float32)
-    dst = torch.empty_like(src)
-    assert copy_tensor_chunked(src, dst, chunk_bytes=400) == 10
-    assert torch.equal(src, dst)
-    with pytest.raises(ValueError):
-        copy_tensor_chunked(src, torch.empty(999))
-    with pytest.raises(ValueError):
-        copy_tensor_chunked(src, torch.empty(1000, dtype=torch.float16))
-    with pytest.raises(ValueError):
-        copy_tensor_chunked(src, dst, chunk_bytes=0)
-
-
 # ------------------------------------------------- prepare_nf4 (quantizer stubbed)
 class _Recorder:
     """Stand-in for the GPU quantizer: records the 2-D shape it receives."""
