@@ -1,34 +1,30 @@
 """Frozen SwiGLU MLP with a token-chunked forward and a chunk-by-chunk
-backward recompute, with an NF4 fast path for MI355X.
+recompute in the backward, with an NF4 fast path for MI355X.
 
-Same module and autograd function as the reference's memory-flat frozen MLP
+Interface of the reference's memory-flat frozen MLP
 (``stratum/model/mlp_opt.py:103-245``): ``MemoryFlatFrozenMLP(module,
-token_chunk_size)`` wraps a frozen dense MLP ``down(act_fn(gate(x)) * up(x))``
-with either Qwen (``gate_proj``/``up_proj``/``down_proj``) or LFM2.5
-(``ffn_*_proj``) projection names, runs the forward over token chunks without
-keeping the 3x-hidden intermediate, and recomputes one chunk at a time in the
-backward to produce the input gradient (the parameters are frozen).
+token_chunk_size)`` wraps a frozen MLP ``down(act_fn(gate(x)) * up(x))`` with
+either Qwen (``gate_proj``/``up_proj``/``down_proj``) or LFM2.5 (``ffn_*_proj``)
+projection names, never holds the whole ``[tokens, intermediate]`` activation,
+and recomputes one chunk at a time in the backward to produce the input
+gradient (the parameters are frozen).
 
-When the three projections are :class:`~stratum_amd.nf4_linear.NF4Linear`
-(packed NF4 weights resident on the GPU) the chunk math runs on the HIP
-library instead of autograd:
+Here the MLP is treated as a function of token rows: the input is flattened to
+``[rows, hidden]`` and processed ``token_chunk_size * batch`` rows at a time
+(each token's result does not depend on the chunking). Two row engines do the
+work:
 
-* gate and up are stacked once into one packed payload ``[2 I, H]`` (NF4 rows
-  are independent: the stack is the byte concatenation of the two payloads and
-  of their absmax), so each is ONE fused dequant-GEMM with N = 2 I;
-* ``silu(gate) * up`` and its gradient are single HIP passes (``swiglu_fwd``,
-  ``swiglu_bwd``) in fp32 with one rounding;
-* the backward of a chunk is ``gu = X Wguᵀ`` (recompute), ``dh = dY Wd``,
-  ``dgu = swiglu_bwd(dh, gu)``, ``dX = dgu Wgu``: five GEMM units of
-  ``2·rows·H·I`` flops against the reference's six (it also recomputes the
-  down projection's output, which the input gradient does not need);
-* chunks larger than ``fused_max_rows()`` rows dequantize the stacked weights
-  once per call and run those GEMMs on the library (see ``nf4_linear``).
-
-Chunks are taken over the flattened tokens, ``token_chunk_size`` tokens of
-every batch row at a time, so the peak intermediate is the reference's
-(``token_chunk_size · batch · 2 I``); the MLP is positionwise, so each token's
-result does not depend on the chunking.
+* ``NF4StackedMLP`` when the projections are :class:`NF4Linear` (packed
+  weights resident on the GPU) with a SiLU gate: gate and up are one stacked
+  ``[2 I, H]`` payload (``quantize_mlp_`` quantizes them into one buffer and
+  the two NF4Linear hold views of it, so nothing is duplicated), each
+  projection pair is ONE fused dequant-GEMM, ``silu(g) * u`` and its gradient
+  are single HIP passes, and the input gradient of a chunk is
+  ``dX = swiglu_bwd(dY Wd, X Wguᵀ) Wgu`` -- five GEMM units per chunk, against
+  six for a recompute through autograd (which also recomputes the down
+  projection's output);
+* ``_ModuleRows`` otherwise: the module's own projections, with the input
+  gradient of a chunk taken by a backward pass over that chunk's recompute.
 """
 
 from __future__ import annotations
@@ -38,8 +34,8 @@ from typing import Any, NamedTuple, Optional
 import torch
 import torch.nn as nn
 
-from .functional import (dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit, swiglu_bwd,
-                         swiglu_fwd)
+from .functional import (QuantState, dequantize_4bit, fused_supported, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit,
+                         swiglu_bwd, swiglu_fwd)
 from .nf4_linear import NF4Linear, fused_max_rows
 
 __all__ = [
@@ -60,39 +56,53 @@ def _mlp_projection_names(module: nn.Module) -> _MlpProjectionNames:
     """Projection attribute names of a dense MLP (``stratum/model/mlp_opt.py:109-115``)."""
     if hasattr(module, "gate_exps"):
         raise TypeError("memory-flat frozen MLP does not support MoE expert modules")
-    if hasattr(module, "ffn_gate_proj"):
-        return _MlpProjectionNames("ffn_gate_proj", "ffn_up_proj", "ffn_down_proj")
-    return _MlpProjectionNames("gate_proj", "up_proj", "down_proj")
+    prefix = "ffn_" if hasattr(module, "ffn_gate_proj") else ""
+    return _MlpProjectionNames(f"{prefix}gate_proj", f"{prefix}up_proj", f"{prefix}down_proj")
 
 
 def _assert_frozen_mlp(module: nn.Module) -> _MlpProjectionNames:
-    """Validate a frozen dense MLP (``stratum/model/mlp_opt.py:118-151``).
-
-    Projections may be ``nn.Linear`` (dense weights) or ``NF4Linear`` (packed
-    NF4 weights); the errors are the reference's.
-    """
-    proj_names = _mlp_projection_names(module)
-    missing = [name for name in proj_names if not hasattr(module, name)]
+    """Check that *module* is a frozen, bias-free gate/up/down MLP with an
+    ``act_fn``; projections may be ``nn.Linear`` or ``NF4Linear``. Exception types
+    and messages follow ``stratum/model/mlp_opt.py:118-151``."""
+    names = _mlp_projection_names(module)
+    missing = [n for n in names if not hasattr(module, n)]
     if missing:
         raise TypeError(f"memory-flat frozen MLP requires gate/up/down projections, missing: {missing}")
     if not hasattr(module, "act_fn"):
         raise TypeError("memory-flat frozen MLP requires act_fn (SiLU)")
-    trainable = [name for name, param in module.named_parameters() if param.requires_grad]
+    trainable = [n for n, p in module.named_parameters() if p.requires_grad]
     if trainable:
         raise ValueError("--memory-flat-frozen-mlp only supports frozen MLP parameters; "
                          f"trainable parameters found: {trainable[:8]}")
-    for name in proj_names:
-        proj = getattr(module, name)
+    for n in names:
+        proj = getattr(module, n)
         if not isinstance(proj, (nn.Linear, NF4Linear)):
-            raise TypeError(f"memory-flat frozen MLP expected {name} to be nn.Linear, got {type(proj)!r}")
+            raise TypeError(f"memory-flat frozen MLP expected {n} to be nn.Linear, got {type(proj)!r}")
         if proj.bias is not None:
-            raise TypeError(f"memory-flat frozen MLP currently expects bias=False for {name}")
-    return proj_names
+            raise TypeError(f"memory-flat frozen MLP currently expects bias=False for {n}")
+    return names
+
+
+def _adjacent_view(a: torch.Tensor, b: torch.Tensor) -> Optional[torch.Tensor]:
+    """A flat view covering *a* then *b* when *b* starts right where *a* ends in
+    the same storage (both contiguous); None otherwise."""
+    if not (a.is_contiguous() and b.is_contiguous() and a.dtype == b.dtype and a.device == b.device):
+        return None
+    if a.untyped_storage().data_ptr() != b.untyped_storage().data_ptr():
+        return None
+    if b.storage_offset() != a.storage_offset() + a.numel():
+        return None
+    return a.new_empty(0).set_(a.untyped_storage(), a.storage_offset(), (a.numel() + b.numel(),))
 
 
 class NF4StackedMLP:
-    """Device-resident packed weights of an NF4 SwiGLU MLP: ``[gate; up]``
-    stacked into one ``[2 I, H]`` payload, and ``down`` ``[H, I]``."""
+    """Device-resident packed weights of an NF4 SwiGLU MLP as the kernels take
+    them: ``[gate; up]`` as one ``[2 I, H]`` payload and ``down`` ``[H, I]``.
+
+    When gate and up are adjacent views of one buffer (``quantize_mlp_``) the
+    stacked payload is a view of it; otherwise it is one concatenated copy,
+    rebuilt when any source tensor changes (identity or in-place version).
+    """
 
     def __init__(self, gate: NF4Linear, up: NF4Linear, down: NF4Linear):
         gs, us, ds = gate.quant_state, up.quant_state, down.quant_state
@@ -102,66 +112,91 @@ class NF4StackedMLP:
         if not (gs.blocksize == us.blocksize == ds.blocksize):
             raise ValueError("gate, up and down must share one blocksize")
         self.hidden, self.inter, self.blocksize = hidden, inter, gs.blocksize
-        self.gu_packed = torch.cat([gate.quantized.reshape(-1), up.quantized.reshape(-1)])
-        self.gu_absmax = torch.cat([gs.absmax.reshape(-1), us.absmax.reshape(-1)]).float()
+        gq, uq = gate.quantized.reshape(-1), up.quantized.reshape(-1)
+        ga, ua = gs.absmax.reshape(-1), us.absmax.reshape(-1)
+        self.gu_packed = _adjacent_view(gq, uq)
+        self.gu_absmax = _adjacent_view(ga, ua) if ga.dtype == torch.float32 else None
+        self.shares_storage = self.gu_packed is not None and self.gu_absmax is not None
+        if not self.shares_storage:
+            self.gu_packed = torch.cat([gq, uq])
+            self.gu_absmax = torch.cat([ga, ua]).float()
         self.d_packed = down.quantized.reshape(-1)
         self.d_absmax = ds.absmax.reshape(-1).float()
-        self.key = (gate.quantized.data_ptr(), up.quantized.data_ptr(), down.quantized.data_ptr())
+        self.key = self.source_key(gate, up, down)
+
+    @staticmethod
+    def source_key(gate: NF4Linear, up: NF4Linear, down: NF4Linear) -> tuple:
+        ts = (gate.quantized, up.quantized, down.quantized, gate.quant_state.absmax, up.quant_state.absmax,
+              down.quant_state.absmax)
+        return tuple((id(t), t._version) for t in ts)
 
     @staticmethod
     def supported(hidden: int, inter: int, blocksize: int) -> bool:
         return (fused_supported(2 * inter, hidden, blocksize, backward=True)
                 and fused_supported(hidden, inter, blocksize, backward=True))
 
-    def _fused(self, rows_per_chunk: int) -> bool:
-        limit = fused_max_rows()
-        return limit < 0 or rows_per_chunk <= limit
-
-    def _dense(self, dtype: torch.dtype):
-        """Dequantized [2 I, H] and [H, I] temporaries for the library-GEMM path."""
+    def _library_weights(self, dtype: torch.dtype):
+        """Dequantized [2 I, H] and [H, I] temporaries for chunks above the fused
+        kernels' row range (dequantized once per call, library GEMMs)."""
         H, I, bs = self.hidden, self.inter, self.blocksize
-        w_gu = dequantize_4bit(self.gu_packed, absmax=self.gu_absmax, blocksize=bs, dtype=dtype, shape=(2 * I, H))
-        w_d = dequantize_4bit(self.d_packed, absmax=self.d_absmax, blocksize=bs, dtype=dtype, shape=(H, I))
-        return w_gu, w_d
+        return (dequantize_4bit(self.gu_packed, absmax=self.gu_absmax, blocksize=bs, dtype=dtype, shape=(2 * I, H)),
+                dequantize_4bit(self.d_packed, absmax=self.d_absmax, blocksize=bs, dtype=dtype, shape=(H, I)))
 
     def forward_rows(self, x: torch.Tensor, out: torch.Tensor, rows_per_chunk: int) -> None:
-        """``out[r] = down(silu(gate(x[r])) * up(x[r]))`` for the rows of ``x`` [rows, H].
-
-        Chunks of at most ``fused_max_rows()`` rows run the fused kernels; larger
-        chunks dequantize the stacked weights once for the whole call and run
-        the library GEMM (the faster choice there, see ``nf4_linear``).
-        """
+        """``out = down(silu(gate(x)) * up(x))`` for x [rows, H], chunk by chunk."""
         H, I, bs = self.hidden, self.inter, self.blocksize
-        if not self._fused(rows_per_chunk):
-            w_gu, w_d = self._dense(x.dtype)
+        limit = fused_max_rows()
+        if limit < 0 or rows_per_chunk <= limit:
             for s in range(0, x.shape[0], rows_per_chunk):
-                e = min(s + rows_per_chunk, x.shape[0])
-                h = swiglu_fwd(x[s:e] @ w_gu.t())
-                torch.matmul(h, w_d.t(), out=out[s:e])
+                c = slice(s, s + rows_per_chunk)
+                h = swiglu_fwd(nf4_gemm_fwd(x[c], self.gu_packed, self.gu_absmax, (2 * I, H), bs))
+                nf4_gemm_fwd(h, self.d_packed, self.d_absmax, (H, I), bs, out=out[c])
             return
+        w_gu, w_d = self._library_weights(x.dtype)
         for s in range(0, x.shape[0], rows_per_chunk):
-            e = min(s + rows_per_chunk, x.shape[0])
-            gu = nf4_gemm_fwd(x[s:e], self.gu_packed, self.gu_absmax, (2 * I, H), bs)
-            h = swiglu_fwd(gu)
-            nf4_gemm_fwd(h, self.d_packed, self.d_absmax, (H, I), bs, out=out[s:e])
+            c = slice(s, s + rows_per_chunk)
+            torch.mm(swiglu_fwd(torch.mm(x[c], w_gu.t())), w_d.t(), out=out[c])
 
     def input_grad_rows(self, x: torch.Tensor, dy: torch.Tensor, dx: torch.Tensor, rows_per_chunk: int) -> None:
-        """``dx[r]`` = gradient of the MLP output row r (given ``dy[r]``) with respect to ``x[r]``."""
+        """``dx`` = gradient of the MLP output rows (``dy``) with respect to ``x``."""
         H, I, bs = self.hidden, self.inter, self.blocksize
-        if not self._fused(rows_per_chunk):
-            w_gu, w_d = self._dense(x.dtype)
+        limit = fused_max_rows()
+        if limit < 0 or rows_per_chunk <= limit:
             for s in range(0, x.shape[0], rows_per_chunk):
-                e = min(s + rows_per_chunk, x.shape[0])
-                gu = x[s:e] @ w_gu.t()
-                dgu = swiglu_bwd(dy[s:e] @ w_d, gu)
-                torch.matmul(dgu, w_gu, out=dx[s:e])
+                c = slice(s, s + rows_per_chunk)
+                gu = nf4_gemm_fwd(x[c], self.gu_packed, self.gu_absmax, (2 * I, H), bs)
+                dgu = swiglu_bwd(nf4_gemm_bwd_dx(dy[c], self.d_packed, self.d_absmax, (H, I), bs), gu)
+                nf4_gemm_bwd_dx(dgu, self.gu_packed, self.gu_absmax, (2 * I, H), bs, out=dx[c])
             return
+        w_gu, w_d = self._library_weights(x.dtype)
         for s in range(0, x.shape[0], rows_per_chunk):
-            e = min(s + rows_per_chunk, x.shape[0])
-            gu = nf4_gemm_fwd(x[s:e], self.gu_packed, self.gu_absmax, (2 * I, H), bs)
-            dh = nf4_gemm_bwd_dx(dy[s:e], self.d_packed, self.d_absmax, (H, I), bs)
-            dgu = swiglu_bwd(dh, gu)
-            nf4_gemm_bwd_dx(dgu, self.gu_packed, self.gu_absmax, (2 * I, H), bs, out=dx[s:e])
+            c = slice(s, s + rows_per_chunk)
+            dgu = swiglu_bwd(torch.mm(dy[c], w_d), torch.mm(x[c], w_gu.t()))
+            torch.mm(dgu, w_gu, out=dx[c])
+
+
+class _ModuleRows:
+    """Row engine over the module's own projections (any act_fn)."""
+
+    def __init__(self, module: nn.Module, names: _MlpProjectionNames):
+        self.gate, self.up, self.down = (getattr(module, n) for n in names)
+        self.act = module.act_fn
+
+    def _mlp(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down(self.act(self.gate(x)) * self.up(x))
+
+    def forward_rows(self, x: torch.Tensor, out: torch.Tensor, rows_per_chunk: int) -> None:
+        with torch.no_grad():
+            for s in range(0, x.shape[0], rows_per_chunk):
+                out[s:s + rows_per_chunk] = self._mlp(x[s:s + rows_per_chunk])
+
+    def input_grad_rows(self, x: torch.Tensor, dy: torch.Tensor, dx: torch.Tensor, rows_per_chunk: int) -> None:
+        for s in range(0, x.shape[0], rows_per_chunk):
+            c = slice(s, s + rows_per_chunk)
+            with torch.enable_grad():
+                leaf = x[c].detach().requires_grad_(True)
+                self._mlp(leaf).backward(dy[c])
+            dx[c] = leaf.grad
 
 
 _STACK_ATTR = "_stratum_nf4_stack"
@@ -169,31 +204,29 @@ _SILU_PROBE = torch.tensor([-6.0, -1.25, -0.5, 0.0, 0.75, 2.0, 9.0])
 
 
 def _is_silu(act) -> bool:
-    """``act`` computes SiLU (``nn.SiLU``, transformers' ``SiLUActivation``, ...): checked once
-    on a few CPU values, cached on the object."""
+    """``act`` computes SiLU (``nn.SiLU``, transformers' ``SiLUActivation``, ...):
+    checked once on a few CPU values and remembered on the object."""
     if isinstance(act, nn.SiLU):
         return True
-    cached = getattr(act, "_stratum_is_silu", None)
-    if cached is None:
+    known = getattr(act, "_stratum_is_silu", None)
+    if known is None:
         try:
             with torch.no_grad():
-                cached = bool(torch.allclose(act(_SILU_PROBE.clone()), nn.functional.silu(_SILU_PROBE),
-                                             rtol=1e-6, atol=1e-7))
+                known = bool(torch.allclose(act(_SILU_PROBE.clone()), nn.functional.silu(_SILU_PROBE),
+                                            rtol=1e-6, atol=1e-7))
         except Exception:
-            cached = False
+            known = False
         try:
-            object.__setattr__(act, "_stratum_is_silu", cached)
+            object.__setattr__(act, "_stratum_is_silu", known)
         except (AttributeError, TypeError):
             pass
-    return cached
+    return known
 
 
 def _nf4_stack(module: nn.Module, names: _MlpProjectionNames, x: torch.Tensor) -> Optional[NF4StackedMLP]:
-    """The NF4 fast path for ``module`` and input ``x``, or None when it does not apply."""
+    """The NF4 row engine for *module* and input *x*, or None when it does not apply."""
     gate, up, down = (getattr(module, n) for n in names)
-    if not (isinstance(gate, NF4Linear) and isinstance(up, NF4Linear) and isinstance(down, NF4Linear)):
-        return None
-    if not _is_silu(module.act_fn):
+    if not all(isinstance(p, NF4Linear) for p in (gate, up, down)) or not _is_silu(module.act_fn):
         return None
     if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)):
         return None
@@ -203,81 +236,55 @@ def _nf4_stack(module: nn.Module, names: _MlpProjectionNames, x: torch.Tensor) -
     if x.shape[-1] != hidden or not NF4StackedMLP.supported(hidden, inter, gate.quant_state.blocksize):
         return None
     stack = getattr(module, _STACK_ATTR, None)
-    key = (gate.quantized.data_ptr(), up.quantized.data_ptr(), down.quantized.data_ptr())
-    if stack is None or stack.key != key:
+    if stack is None or stack.key != NF4StackedMLP.source_key(gate, up, down):
         stack = NF4StackedMLP(gate, up, down)
-        object.__setattr__(module, _STACK_ATTR, stack)  # not a submodule / parameter
+        object.__setattr__(module, _STACK_ATTR, stack)  # not a submodule, not state
     return stack
 
 
+def _rows_engine(module: nn.Module, names: _MlpProjectionNames, x: torch.Tensor):
+    return _nf4_stack(module, names, x) or _ModuleRows(module, names)
+
+
 def _rows_per_chunk(hidden_states: torch.Tensor, token_chunk_size: int) -> int:
-    batch = 1
+    """token_chunk_size tokens of every leading (batch) row."""
+    lead = 1
     for d in hidden_states.shape[:-2]:
-        batch *= int(d)
-    return max(1, token_chunk_size * batch)
+        lead *= int(d)
+    return max(1, token_chunk_size * lead)
 
 
 class MemoryFlatFrozenMLPFunction(torch.autograd.Function):
-    """Custom autograd: forward runs the MLP in chunks, backward recomputes one
-    chunk at a time (``stratum/model/mlp_opt.py:154-215``)."""
+    """Chunked forward; the backward recomputes and differentiates one chunk at a
+    time (``stratum/model/mlp_opt.py:154-215``)."""
 
     @staticmethod
     def forward(ctx: Any, hidden_states: torch.Tensor, module: nn.Module, token_chunk_size: int) -> torch.Tensor:
-        proj_names = _assert_frozen_mlp(module)
+        names = _assert_frozen_mlp(module)
         if token_chunk_size <= 0:
             raise ValueError("token_chunk_size must be positive")
         if hidden_states.dim() < 3:
             raise ValueError("memory-flat frozen MLP expects [batch, seq, hidden] input")
-
-        ctx.module = module
-        ctx.proj_names = proj_names
-        ctx.token_chunk_size = token_chunk_size
+        engine = _rows_engine(module, names, hidden_states)
+        rows = _rows_per_chunk(hidden_states, token_chunk_size)
+        x = hidden_states.reshape(-1, hidden_states.shape[-1]).contiguous()
+        out_features = getattr(module, names.down).out_features
+        out = x.new_empty(x.shape[0], out_features)
+        engine.forward_rows(x, out, rows)
+        ctx.engine, ctx.rows = engine, rows
         ctx.save_for_backward(hidden_states)
-
-        stack = _nf4_stack(module, proj_names, hidden_states)
-        ctx.stack = stack
-        if stack is not None:
-            x = hidden_states.reshape(-1, stack.hidden).contiguous()
-            out = torch.empty_like(x)
-            stack.forward_rows(x, out, _rows_per_chunk(hidden_states, token_chunk_size))
-            return out.reshape(hidden_states.shape)
-
-        seq_len = hidden_states.shape[1]
-        gate_proj, up_proj, down_proj = (getattr(module, n) for n in proj_names)
-        output = hidden_states.new_empty(*hidden_states.shape[:-1], down_proj.out_features)
-        with torch.no_grad():
-            for start in range(0, seq_len, token_chunk_size):
-                end = min(start + token_chunk_size, seq_len)
-                chunk = hidden_states[:, start:end, :]
-                output[:, start:end, :] = down_proj(module.act_fn(gate_proj(chunk)) * up_proj(chunk))
-        return output
+        return out.reshape(*hidden_states.shape[:-1], out_features)
 
     @staticmethod
-    def backward(ctx: Any, grad_output: torch.Tensor) -> tuple[Optional[torch.Tensor], None, None]:
-        (hidden_states,) = ctx.saved_tensors
+    def backward(ctx: Any, grad_output: torch.Tensor):
         if not ctx.needs_input_grad[0]:
             return None, None, None
-        module, proj_names, token_chunk_size = ctx.module, ctx.proj_names, ctx.token_chunk_size
-        stack = ctx.stack
-        if stack is not None:
-            x = hidden_states.reshape(-1, stack.hidden).contiguous()
-            dy = grad_output.reshape(-1, stack.hidden).contiguous()
-            dx = torch.empty_like(x)
-            stack.input_grad_rows(x, dy, dx, _rows_per_chunk(hidden_states, token_chunk_size))
-            return dx.reshape(hidden_states.shape), None, None
-
-        seq_len = hidden_states.shape[1]
-        grad_hidden_states = torch.empty_like(hidden_states)
-        gate_proj, up_proj, down_proj = (getattr(module, n) for n in proj_names)
-        with torch.enable_grad():
-            for start in range(0, seq_len, token_chunk_size):
-                end = min(start + token_chunk_size, seq_len)
-                chunk = hidden_states[:, start:end, :].detach().requires_grad_(True)
-                chunk_output = down_proj(module.act_fn(gate_proj(chunk)) * up_proj(chunk))
-                (grad_chunk,) = torch.autograd.grad(chunk_output, chunk, grad_outputs=grad_output[:, start:end, :],
-                                                    retain_graph=False, create_graph=False)
-                grad_hidden_states[:, start:end, :] = grad_chunk
-        return grad_hidden_states, None, None
+        (hidden_states,) = ctx.saved_tensors
+        x = hidden_states.reshape(-1, hidden_states.shape[-1]).contiguous()
+        dy = grad_output.reshape(x.shape[0], -1).contiguous()
+        dx = torch.empty_like(x)
+        ctx.engine.input_grad_rows(x, dy, dx, ctx.rows)
+        return dx.reshape(hidden_states.shape), None, None
 
 
 class MemoryFlatFrozenMLP(nn.Module):
@@ -295,6 +302,8 @@ class MemoryFlatFrozenMLP(nn.Module):
         if args or kwargs:
             raise ValueError("MemoryFlatFrozenMLP only supports a hidden_states positional argument")
         if hidden_states.shape[1] <= self.token_chunk_size and not hidden_states.requires_grad:
+            # nothing to save for a backward and one chunk: the NF4 engine in one
+            # pass, or the module itself
             stack = _nf4_stack(self.module, _mlp_projection_names(self.module), hidden_states)
             if stack is None:
                 return self.module(hidden_states)
@@ -314,17 +323,40 @@ class MemoryFlatFrozenMLP(nn.Module):
 
 @torch.no_grad()
 def quantize_mlp_(module: nn.Module, device: Optional[torch.device] = None, blocksize: int = 64) -> nn.Module:
-    """Replace the dense gate/up/down ``nn.Linear`` of ``module`` with NF4Linear
-    (quantized on the GPU, packed weights resident on ``device``). In place."""
+    """Replace the dense gate/up/down ``nn.Linear`` of *module* with NF4Linear
+    (quantized on the GPU, packed weights resident on *device*), in place.
+
+    Gate and up are quantized together as one ``[2 I, H]`` weight (NF4 rows are
+    independent and a block never straddles a row when H is a multiple of the
+    blocksize, so the bytes equal two separate quantizations); the two
+    NF4Linear hold views of that one payload, which the fused MLP path uses
+    without copying."""
     names = _mlp_projection_names(module)
+    gate, up = getattr(module, names.gate), getattr(module, names.up)
+    for name in names:
+        lin = getattr(module, name)
+        if not isinstance(lin, (nn.Linear, NF4Linear)) or (isinstance(lin, nn.Linear) and lin.bias is not None):
+            raise TypeError(f"{name} must be a bias-free nn.Linear")
+
+    def target(w: torch.Tensor) -> torch.device:
+        return torch.device(device) if device is not None else (w.device if w.is_cuda else torch.device("cuda"))
+
+    if (type(gate) is nn.Linear and type(up) is nn.Linear and gate.weight.shape == up.weight.shape
+            and gate.weight.shape[1] % blocksize == 0):
+        inter, hidden = gate.weight.shape
+        dev = target(gate.weight)
+        stacked = torch.cat([gate.weight.detach().to(dev), up.weight.detach().to(dev)])
+        packed, state = quantize_4bit(stacked, blocksize=blocksize)
+        half_q, half_a = inter * hidden // 2, inter * hidden // blocksize
+        for name, sl_q, sl_a in ((names.gate, slice(0, half_q), slice(0, half_a)),
+                                 (names.up, slice(half_q, 2 * half_q), slice(half_a, 2 * half_a))):
+            st = QuantState(absmax=state.absmax[sl_a], shape=(inter, hidden), code=state.code,
+                            blocksize=blocksize, quant_type=state.quant_type, dtype=state.dtype)
+            setattr(module, name, NF4Linear(packed[sl_q], st))
     for name in names:
         lin = getattr(module, name)
         if isinstance(lin, NF4Linear):
             continue
-        if not isinstance(lin, nn.Linear) or lin.bias is not None:
-            raise TypeError(f"{name} must be a bias-free nn.Linear")
-        w = lin.weight.detach()
-        dev = torch.device(device) if device is not None else (w.device if w.is_cuda else torch.device("cuda"))
-        packed, state = quantize_4bit(w.to(dev), blocksize=blocksize)
+        packed, state = quantize_4bit(lin.weight.detach().to(target(lin.weight)), blocksize=blocksize)
         setattr(module, name, NF4Linear(packed, state))
     return module

@@ -180,3 +180,30 @@ def test_nf4_mlp_unsupported_shape_falls_back_to_module_math(cuda):
     yr = F.linear(F.silu(F.linear(xr, W["gate_proj"])) * F.linear(xr, W["up_proj"]), W["down_proj"])
     yr.sum().backward()
     assert rel(y, yr) < 1e-2 and rel(x.grad, xr.grad) < 1e-2
+
+
+def test_quantize_mlp_stacks_gate_and_up_without_a_copy(cuda):
+    """quantize_mlp_ quantizes gate and up as one [2 I, H] weight: each half is
+    bit-exact to the oracle's quantization of that projection alone, the two
+    NF4Linear hold views of the one buffer, and the fused MLP path uses it
+    without concatenating a copy; an in-place change to a payload rebuilds the
+    stacked view's key."""
+    from stratum_amd.mlp import NF4StackedMLP, _nf4_stack, _mlp_projection_names, quantize_mlp_
+    H, I = 512, 1536
+    dense = DenseMlp(H, I, torch.bfloat16, cuda, seed=11)
+    src = {n: getattr(dense, n).weight.detach().cpu().clone() for n in ("gate_proj", "up_proj", "down_proj")}
+    mlp = quantize_mlp_(dense)
+    for n, w in src.items():
+        bits = w.contiguous().view(torch.int16).numpy().view(np.uint16)
+        rp, ra = C.quantize(bits, O.DT_BF16, 64, "argmin")
+        lin = getattr(mlp, n)
+        np.testing.assert_array_equal(lin.quantized.cpu().numpy().ravel(), rp)
+        np.testing.assert_array_equal(lin.quant_state.absmax.cpu().numpy().view(np.uint32), ra.view(np.uint32))
+    gq, uq = mlp.gate_proj.quantized, mlp.up_proj.quantized
+    assert gq.untyped_storage().data_ptr() == uq.untyped_storage().data_ptr()
+    x = torch.randn(1, 8, H, device=cuda).to(torch.bfloat16)
+    stack = _nf4_stack(mlp, _mlp_projection_names(mlp), x)
+    assert isinstance(stack, NF4StackedMLP) and stack.shares_storage
+    assert stack.gu_packed.data_ptr() == gq.data_ptr() and stack.gu_packed.numel() == gq.numel() + uq.numel()
+    mlp.down_proj.quant_state.absmax.mul_(1.0)  # in place: version bump
+    assert _nf4_stack(mlp, _mlp_projection_names(mlp), x) is not stack
