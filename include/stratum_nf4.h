@@ -106,6 +106,24 @@ int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, 
                      int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * stm_nf4_gemm_fwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split-reduction partials that stm_nf4_gemm_fwd keeps in
+ * the caller's workspace go to a static 16 MiB device array of the library
+ * (one per GPU, held until the process ends; its address is looked up once per
+ * device on the first call there, on the current device). Problems whose
+ * partials need more than 16 MiB (stm_nf4_gemm_workspace_bytes(M, N, K, 0) >
+ * 16 MiB) return STM_ERR_UNSUPPORTED. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (concurrent streams or threads) race. The
+ * partials are fully overwritten by each call (nothing needs clearing).
+ * Arguments, constraints and results otherwise as stm_nf4_gemm_fwd.
+ */
+int stm_nf4_gemm_fwd_noalloc(const void* X, const uint8_t* packed, const float* absmax, const void* bias,
+                             const void* T, const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K,
+                             int blocksize, int dtype, void* stream);
+
+/*
  * Fused NF4 dequant-GEMM, input gradient of a frozen Linear (no dW: the base
  * weight has requires_grad=False, stratum/upload.py:328-329):
  *   dX[M, K] = dY[M, N] . W[N, K]  (+ U[M, R] . At[K, R]^T)

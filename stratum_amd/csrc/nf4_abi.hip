@@ -5,6 +5,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "nf4_common.h"
 #include "nf4_kernels.h"
 
@@ -110,6 +113,42 @@ static bool is_16bit(int dt) { return dt == STM_F16 || dt == STM_BF16; }
 static bool valid_dtype(int dt) { return dt == STM_F16 || dt == STM_BF16 || dt == STM_F32; }
 static bool valid_blocksize(int bs) { return bs >= 64 && bs <= 4096 && is_pow2(bs); }
 
+// ------------------------------------------------- allocation-free scratch
+// Device memory of stm_nf4_gemm_fwd_noalloc: the fp32 split-reduction partials
+// that stm_nf4_gemm_fwd takes from the caller's workspace. One array per GPU
+// (each device holds its own copy of a __device__ variable, for the life of
+// the process). In host code `scratch` names a host-side stand-in, not a
+// device address: kernels receive the per-device address that
+// hipGetSymbolAddress returns, fetched once per device.
+constexpr int64_t kScratchBytes = (int64_t)16 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The scratch address on the current device (fetched on the first call there).
+static int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(STM_ERR_HIP, "gemm_fwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd_noalloc: device %d", dev);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return set_error(STM_ERR_HIP, "gemm_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                                 hipGetErrorString(e));
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return STM_OK;
+}
+
 }  // namespace stm
 
 using namespace stm;
@@ -214,6 +253,36 @@ int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, 
     g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
     g.partial = need ? (float*)workspace : nullptr;
+    return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
+}
+
+int stm_nf4_gemm_fwd_noalloc(const void* X, const uint8_t* packed, const float* absmax, const void* bias,
+                             const void* T, const void* L, int lora_rank, void* Y, int64_t M, int64_t N, int64_t K,
+                             int blocksize, int dtype, void* stream) {
+    g_err[0] = 0;
+    int rc = check_gemm_common("gemm_fwd_noalloc", X, packed, absmax, Y, M, N, K, blocksize, dtype);
+    if (rc <= 0) return rc;
+    if (N % 8 != 0)
+        return set_error(STM_ERR_UNSUPPORTED, "gemm_fwd_noalloc: N = %lld must be a multiple of 8", (long long)N);
+    if (lora_rank < 0 || lora_rank % 16 != 0 || lora_rank > 256)
+        return set_error(STM_ERR_INVALID, "gemm_fwd_noalloc: lora_rank %d must be a multiple of 16 in [0, 256]",
+                         lora_rank);
+    if (lora_rank > 0 && (!T || !L || !aligned(T, 16) || !aligned(L, 16)))
+        return set_error(STM_ERR_INVALID, "gemm_fwd_noalloc: lora_rank > 0 needs 16-byte aligned T and L");
+    if (bias && !aligned(bias, 2)) return set_error(STM_ERR_INVALID, "gemm_fwd_noalloc: misaligned bias");
+    const int64_t need = gemm_workspace_bytes(M, N, K, false, 1);
+    if (need > kScratchBytes)
+        return set_error(STM_ERR_UNSUPPORTED,
+                         "gemm_fwd_noalloc: this %lld x %lld x %lld problem splits its reduction into %lld bytes of "
+                         "partials, more than the %lld-byte static scratch; call stm_nf4_gemm_fwd with a workspace",
+                         (long long)M, (long long)N, (long long)K, (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    if (need > 0 && (rc = scratch_address(&ws)) != STM_OK) return rc;
+    GemmArgs g{};
+    g.a = X; g.packed = packed; g.absmax = absmax; g.bias = bias; g.lora_x = lora_rank ? T : nullptr;
+    g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
+    g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
+    g.partial = need ? (float*)ws : nullptr;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 

@@ -273,3 +273,18 @@ def test_grouped_gemm_rejects_a_short_payload_and_cpu_operands():
         nf4_grouped_gemm(x, torch.zeros(64 * 64, dtype=torch.uint8), torch.ones(64), off, (64, 64), 64)
     with pytest.raises(RuntimeError, match="GPU"):
         nf4_grouped_gemm(x, torch.zeros(64 * 64, dtype=torch.uint8), torch.ones(128), off, (64, 64), 64)
+
+
+def test_noalloc_forward_refuses_oversized_problems_before_touching_a_gpu(L):
+    """stm_nf4_gemm_fwd_noalloc checks the partials of the split plan against its
+    16 MiB static scratch on the host: an oversized problem is refused with a
+    clear error before any device call (host pointers here)."""
+    buf = ctypes.create_string_buffer(256)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    assert L.stm_nf4_gemm_workspace_bytes(512, 4096, 14336, 0) > 16 << 20
+    assert L.stm_nf4_gemm_fwd_noalloc(p, p, p, None, None, None, 0, p, 512, 4096, 14336, 64, 1, None) == -2
+    assert "static scratch" in _err(L)
+    # the same argument checks as stm_nf4_gemm_fwd
+    assert L.stm_nf4_gemm_fwd_noalloc(p, p, p, None, None, None, 0, p, 16, 4096, 100, 64, 1, None) == -2
+    assert L.stm_nf4_gemm_fwd_noalloc(None, p, p, None, None, None, 0, p, 16, 4096, 128, 64, 1, None) == -1
+    assert L.stm_nf4_gemm_fwd_noalloc(p, p, p, None, None, None, 8, p, 16, 4096, 128, 64, 1, None) == -1
