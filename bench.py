@@ -220,6 +220,30 @@ def run_lora_step(args):
         return xd @ wt.t()
 
     unf_ms = event_time_ms(torch, unfused, reps)
+
+    # fp16, the reference's production training dtype: the same GEMMs
+    x16, dy16 = xd.half(), dy.half()
+    out16 = torch.empty((N, K), dtype=torch.float16, device=dev)
+    fwd16_ms = event_time_ms(torch, lambda: nf4_gemm_fwd(x16, packed, absmax, (N, K), 64), reps)
+    bwd16_ms = event_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy16, packed, absmax, (N, K), 64), reps)
+
+    def unfused16():
+        state.dtype = torch.float16
+        wt = dequantize_4bit(packed, state, out=out16)
+        state.dtype = torch.bfloat16
+        return x16 @ wt.t()
+
+    unf16_ms = event_time_ms(torch, unfused16, reps)
+    del x16, dy16, out16
+    fp16 = {"fwd": {"kernel": "k_gemm_fwd_rw<F16>", "tflops": round(gemm_flops / (fwd16_ms * 1e-3) / 1e12, 2),
+                    "frac": round(gemm_flops / (fwd16_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "avg_kernel_ms": round(fwd16_ms, 4)},
+            "bwd_dx": {"kernel": "k_gemm_bwd_rw<F16>", "tflops": round(gemm_flops / (bwd16_ms * 1e-3) / 1e12, 2),
+                       "frac": round(gemm_flops / (bwd16_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                       "avg_kernel_ms": round(bwd16_ms, 4)},
+            "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt), fp16",
+                            "tflops": round(gemm_flops / (unf16_ms * 1e-3) / 1e12, 2), "ms": round(unf16_ms, 4)},
+            "peak_note": "fp16 dense MFMA peak is the same 2.5 PFLOP/s as bf16"}
     traffic = _profiled_traffic()
     line = {
         "metric": METRIC,
@@ -253,6 +277,7 @@ def run_lora_step(args):
                                 "ms_per_step": round(default_ms, 4),
                                 "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},
         "lora_gflop_per_step": round(lora_flops / 1e9, 2),
+        "fp16": fp16,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, w, N, K, args.cpu_rows)
@@ -318,8 +343,10 @@ def run_roundtrip(torch, args):
 
 
 def run_qwen06(torch, args):
-    """Qwen3-0.6B layer projections, fused NF4 forward at M = 4096 tokens."""
-    from stratum_amd.functional import nf4_gemm_fwd
+    """Qwen3-0.6B layer projections at M = 4096 tokens: fused NF4 forward, and
+    beside it dequantize + hipBLASLt per projection (the reference's
+    architecture, bitsandbytes dequantize then a cuBLAS matmul)."""
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_fwd
     dev = torch.device("cuda:0")
     M = 4096
     shapes = {"q": (2048, 1024), "k": (1024, 1024), "v": (1024, 1024), "o": (1024, 2048),
@@ -327,15 +354,27 @@ def run_qwen06(torch, args):
     ws = {k: _gpu_quantized(torch, s, i, dev) for i, (k, s) in enumerate(shapes.items())}
     xs = {K: seeded(torch, (M, K), 100 + K, 1.0, torch.bfloat16, dev) for K in {s[1] for s in shapes.values()}}
 
+    outs = {k: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for k, (N, K) in shapes.items()}
+    dense = {k: torch.empty(s, dtype=torch.bfloat16, device=dev) for k, s in shapes.items()}
+
     def layer():
         for k, (N, K) in shapes.items():
             p, st = ws[k]
-            nf4_gemm_fwd(xs[K], p, st.absmax, (N, K), 64)
+            nf4_gemm_fwd(xs[K], p, st.absmax, (N, K), 64, out=outs[k])
+
+    def library():  # the reference's architecture: dequantize each weight, then a plain matmul
+        for k, (N, K) in shapes.items():
+            p, st = ws[k]
+            st.dtype = torch.bfloat16
+            torch.matmul(xs[K], dequantize_4bit(p, st, out=dense[k]).t(), out=outs[k])
 
     ms = event_time_ms(torch, layer, 20)
+    lib_ms = event_time_ms(torch, library, 20)
     flops = sum(2.0 * M * N * K for N, K in shapes.values())
     return {"tokens": M, "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
-            "gflop_per_layer": round(flops / 1e9, 2)}
+            "gflop_per_layer": round(flops / 1e9, 2),
+            "dequantize_plus_hipblaslt": {"layer_ms": round(lib_ms, 4), "tflops": round(flops / lib_ms / 1e9, 1)},
+            "fused_speedup": round(lib_ms / ms, 3)}
 
 
 def run_layer_stream(torch, args):
@@ -419,8 +458,9 @@ def run_layer_stream(torch, args):
 
 def run_moe(torch, args):
     """Qwen3-30B-A3B-like expert bank: 128 experts, gate_up [1536, 2048] and
-    down [2048, 768] in NF4; 8192 tokens, top-8 of softmax(N(0,1) logits)."""
-    from stratum_amd.functional import nf4_grouped_gemm
+    down [2048, 768] in NF4; 8192 tokens, top-8 of softmax(N(0,1) logits).
+    Fused grouped GEMMs against dequantize + a per-expert matmul loop."""
+    from stratum_amd.functional import dequantize_4bit, nf4_grouped_gemm
     dev = torch.device("cuda:0")
     E, H, I, T, TOPK = 128, 2048, 768, 8192, 8
     gu_p, gu_s = _gpu_quantized(torch, (E, 2 * I, H), 7, dev)
@@ -436,14 +476,43 @@ def run_moe(torch, args):
     x = seeded(torch, (rows, H), 10, 1.0, torch.bfloat16, dev)
     h = seeded(torch, (rows, I), 11, 1.0, torch.bfloat16, dev)
 
+    offsets = offsets.cpu()  # the host copy: validated and uploaded per call without a device sync
+    y_gu = torch.empty((rows, 2 * I), dtype=torch.bfloat16, device=dev)
+    y_dn = torch.empty((rows, H), dtype=torch.bfloat16, device=dev)
+
     def layer():
-        nf4_grouped_gemm(x, gu_p, gu_s.absmax, offsets, (2 * I, H), 64, max_rows=max_rows)
-        nf4_grouped_gemm(h, dn_p, dn_s.absmax, offsets, (H, I), 64, max_rows=max_rows)
+        nf4_grouped_gemm(x, gu_p, gu_s.absmax, offsets, (2 * I, H), 64, max_rows=max_rows, out=y_gu)
+        nf4_grouped_gemm(h, dn_p, dn_s.absmax, offsets, (H, I), 64, max_rows=max_rows, out=y_dn)
+
+    # the reference's architecture: the staged bank is dequantized whole, then
+    # the experts run one F.linear each per projection (transformers'
+    # Qwen3MoeExperts loop over the experts that received tokens)
+    bounds = offsets.tolist()
+    hit = [e for e in range(E) if bounds[e + 1] > bounds[e]]
+    gu_s.dtype = dn_s.dtype = torch.bfloat16
+    gu_w = torch.empty((E * 2 * I, H), dtype=torch.bfloat16, device=dev)
+    dn_w = torch.empty((E * H, I), dtype=torch.bfloat16, device=dev)
+
+    def expert_loop(gu, dn):
+        for e in hit:
+            r0, r1 = bounds[e], bounds[e + 1]
+            torch.matmul(x[r0:r1], gu[e * 2 * I:(e + 1) * 2 * I].t(), out=y_gu[r0:r1])
+            torch.matmul(h[r0:r1], dn[e * H:(e + 1) * H].t(), out=y_dn[r0:r1])
+
+    def library():
+        expert_loop(dequantize_4bit(gu_p, gu_s, out=gu_w), dequantize_4bit(dn_p, dn_s, out=dn_w))
 
     ms = event_time_ms(torch, layer, 20)
+    lib_ms = event_time_ms(torch, library, 10)
+    loop_ms = event_time_ms(torch, lambda: expert_loop(gu_w, dn_w), 10)
     flops = 2.0 * rows * (2 * I * H + H * I)
     return {"experts": E, "tokens": T, "top_k": TOPK, "rows": rows, "max_rows_per_expert": max_rows,
-            "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1), "gflop_per_layer": round(flops / 1e9, 1)}
+            "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1), "gflop_per_layer": round(flops / 1e9, 1),
+            "dequantize_plus_expert_loop": {"layer_ms": round(lib_ms, 4), "tflops": round(flops / lib_ms / 1e9, 1),
+                                            "what": "k_dequantize over both banks + one hipBLASLt matmul per "
+                                                    "expert and projection"},
+            "expert_loop_dense_only_ms": round(loop_ms, 4),
+            "fused_speedup": round(lib_ms / ms, 3)}
 
 
 def run_mlp(torch, args):

@@ -165,12 +165,24 @@ int stm_nf4_gemm_set_tile(int kind);
  * rows are grouped by expert. Replaces the per-expert F.linear loop of
  * transformers' Qwen3MoeExperts.forward on the dequantized stacked weight.
  *   offsets: device int32 [E + 1], offsets[0] = 0, non-decreasing, offsets[E] = M_total
+ *   host_offsets: NULL, or a host copy of offsets; read before the launch to
+ *             pick the tile height (stm_nf4_grouped_tile_rows). A plan hint
+ *             only: the kernels index rows by the device array alone.
  *   max_rows: an upper bound on offsets[e+1] - offsets[e] (sizes the launch grid)
  *   constraints: as stm_nf4_gemm_fwd
  */
 int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const int32_t* offsets,
-                             int num_experts, int64_t max_rows, void* Y, int64_t N, int64_t K, int blocksize,
-                             int dtype, void* stream);
+                             const int32_t* host_offsets, int num_experts, int64_t max_rows, void* Y, int64_t N,
+                             int64_t K, int blocksize, int dtype, void* stream);
+
+/*
+ * Tile height (192 or 256 rows) the grouped forward uses for these row counts
+ * (host int32 [E + 1] offsets): the height that computes the fewest padded
+ * rows, a 192-row tile's row weighted 8 % dearer. Pure host function; no
+ * counterpart in the reference (its per-expert loop has no tiles).
+ * Returns 192, 256, or STM_ERR_INVALID.
+ */
+int stm_nf4_grouped_tile_rows(const int32_t* host_offsets, int num_experts);
 
 /*
  * Grouped input gradient: for each expert e: dX[rows of e] = dY[rows of e] . W_e.

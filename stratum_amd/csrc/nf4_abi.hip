@@ -309,9 +309,16 @@ int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absm
     return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
 }
 
+int stm_nf4_grouped_tile_rows(const int32_t* host_offsets, int num_experts) {
+    g_err[0] = 0;
+    if (!host_offsets || num_experts <= 0)
+        return set_error(STM_ERR_INVALID, "grouped_tile_rows: NULL offsets or num_experts %d", num_experts);
+    return grouped_tile_rows(host_offsets, num_experts);
+}
+
 int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const int32_t* offsets,
-                             int num_experts, int64_t max_rows, void* Y, int64_t N, int64_t K, int blocksize,
-                             int dtype, void* stream) {
+                             const int32_t* host_offsets, int num_experts, int64_t max_rows, void* Y, int64_t N,
+                             int64_t K, int blocksize, int dtype, void* stream) {
     g_err[0] = 0;
     if (num_experts <= 0 || max_rows < 0)
         return set_error(STM_ERR_INVALID, "grouped_gemm_fwd: num_experts %d, max_rows %lld", num_experts,
@@ -323,6 +330,7 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
     GemmArgs g{};
     g.a = X; g.packed = packed; g.absmax = absmax; g.out = Y; g.M = max_rows; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
+    g.group_bm = host_offsets ? grouped_tile_rows(host_offsets, num_experts) : 0;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 

@@ -2196,6 +2196,17 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
 
 }  // namespace
 
+int grouped_tile_rows(const int32_t* offsets, int num_experts) {
+    int64_t rows256 = 0, rows192 = 0;
+    for (int e = 0; e < num_experts; ++e) {
+        const int64_t r = (int64_t)offsets[e + 1] - offsets[e];
+        if (r <= 0) continue;
+        rows256 += (r + 255) / 256 * 256;
+        rows192 += (r + 191) / 192 * 192;
+    }
+    return (double)rows192 * 1.08 < (double)rows256 ? 192 : 256;
+}
+
 int set_gemm_tile(int kind) {
     return g_tile_only.exchange(kind >= kBig && kind <= kBig8 ? kind : -1, std::memory_order_relaxed);
 }
@@ -2231,7 +2242,9 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
     int rc;
-    if (p.kind == kBig8 && rw_offsets_fit(g))
+    if (p.kind == kBig && g.group_bm == 192 && g.num_groups > 1 && g.splits == 1 && rw && tile_override() < 0)
+        rc = launch_fwd_rw<192, 1>(g, dtype, stream);
+    else if (p.kind == kBig8 && rw_offsets_fit(g))
         rc = launch_fwd_r8(g, dtype, stream);
     else if (p.kind == kMid && rw_offsets_fit(g))
         rc = launch_fwd_rw<128, 1>(g, dtype, stream);

@@ -30,6 +30,9 @@ struct GemmArgs {
     // adds the bias and rounds once.
     float* partial;
     int splits;
+    // Grouped forward: tile height chosen from the host's per-expert row counts
+    // (grouped_tile_rows); 0 = the planner's 256-row tile.
+    int group_bm;
 };
 
 // Split count the launchers use for a problem (1 = no split) and the fp32
@@ -41,6 +44,12 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
 // Restrict the planner to one tile kind (0 = 256 x 256, 1 = 128 x 128,
 // 2 = 128 x 256; anything else = the cost model). Returns the previous setting.
 int set_gemm_tile(int kind);
+
+// Tile height (192 or 256 rows) of the grouped forward for experts with the
+// row counts offsets[e + 1] - offsets[e] (host array of num_experts + 1
+// entries): the one that computes the fewest padded rows, a 192-row row
+// weighted 8 % dearer (its weights are dequantized for fewer rows).
+int grouped_tile_rows(const int32_t* offsets, int num_experts);
 
 int launch_quantize(const void* A, int dtype, int64_t n, int blocksize, const CellTable& tab, uint8_t* packed,
                     float* absmax, hipStream_t stream);

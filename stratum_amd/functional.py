@@ -17,6 +17,7 @@ device).
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from typing import Optional, Sequence
 
 import torch
@@ -312,12 +313,49 @@ def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
     return dx.reshape(*lead, K)
 
 
+_OFFSETS_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_OFFSETS_CACHE_SIZE = 8
+
+
+def _device_offsets(host_off, dev: torch.device):
+    """(pinned host int32 copy, device int32 copy) of validated offsets.
+
+    The values go to the device from pinned memory without a host wait (the
+    caching host allocator keeps the pinned block until the copy has run). The
+    last few arrays are kept per device, so the projections of one MoE layer
+    (gate/up, down, their input gradients) upload their shared offsets once; a
+    hit from another stream waits on the upload's event first.
+    """
+    key = (dev.index, host_off.tobytes())
+    hit = _OFFSETS_CACHE.get(key)
+    stream = torch.cuda.current_stream(dev)
+    if hit is not None:
+        _OFFSETS_CACHE.move_to_end(key)
+        staged, off, done, upload_stream = hit
+        if upload_stream != stream:
+            stream.wait_event(done)
+        return staged, off
+    staged = torch.empty(host_off.shape[0], dtype=torch.int32, pin_memory=True)
+    staged.numpy()[:] = host_off
+    with torch.cuda.device(dev):
+        off = staged.to(dev, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(stream)
+    _OFFSETS_CACHE[key] = (staged, off, done, stream)
+    while len(_OFFSETS_CACHE) > _OFFSETS_CACHE_SIZE:
+        _OFFSETS_CACHE.popitem(last=False)
+    return staged, off
+
+
 @torch.no_grad()
 def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, offsets: torch.Tensor,
                      expert_shape: Sequence[int], blocksize: int = 64, max_rows: Optional[int] = None,
-                     backward: bool = False) -> torch.Tensor:
+                     backward: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-expert ``x[rows_e] @ W_e.T`` (or ``@ W_e`` when ``backward``) over a stacked
     NF4 payload of shape [E, N, K]; ``offsets`` int32 [E + 1] delimits each expert's rows.
+    ``out`` (optional) is a contiguous [rows, N] (backward: [rows, K]) tensor of x's dtype.
+    Offsets given as a CPU tensor are validated and uploaded without a device
+    synchronisation.
 
     The offsets are checked on the host before any launch (one device-to-host
     copy, the synchronisation the grid size needs anyway): ``offsets[0] == 0``,
@@ -336,9 +374,9 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
     xin = _aligned(x)
     M_total = xin.shape[0]
     dev = xin.device
-    host_off = offsets.detach().to("cpu", torch.int64)
+    host_off = offsets.detach().to("cpu", torch.int64).numpy()  # a device array: the one synchronisation
     counts = host_off[1:] - host_off[:-1]
-    if int(host_off[0]) != 0 or bool((counts < 0).any()) or int(host_off[-1]) != M_total:
+    if host_off[0] != 0 or (counts < 0).any() or host_off[-1] != M_total:
         raise ValueError(f"offsets must start at 0, be non-decreasing and end at x.shape[0] = {M_total}; "
                          f"got {host_off.tolist()[:8]}{'...' if E > 7 else ''}")
     largest = int(counts.max())
@@ -352,16 +390,23 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
         raise ValueError(f"absmax holds {absmax.numel()} blocks, {E * N * K // blocksize} needed")
     if not (xin.is_cuda and packed.is_cuda and absmax.is_cuda):
         raise RuntimeError("nf4_grouped_gemm runs on the GPU kernels; x, packed and absmax must be on the GPU")
-    off = host_off.to(device=dev, dtype=torch.int32)
+    staged, off = _device_offsets(host_off, dev)
     out_cols = K if backward else N
     in_cols = N if backward else K
     if xin.shape[1] != in_cols:
         raise ValueError(f"x has {xin.shape[1]} columns, expected {in_cols}")
-    y = torch.empty((M_total, out_cols), dtype=x.dtype, device=dev)
+    if out is None:
+        y = torch.empty((M_total, out_cols), dtype=x.dtype, device=dev)
+    else:
+        if out.shape != (M_total, out_cols) or out.dtype != x.dtype or out.device != dev or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous [{M_total}, {out_cols}] {x.dtype} tensor on {dev}")
+        y = out
     fn = _lib.lib().stm_nf4_grouped_gemm_bwd_dx if backward else _lib.lib().stm_nf4_grouped_gemm_fwd
+    lead = (xin.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(), off.data_ptr())
+    if not backward:  # the host counts pick the forward's tile height
+        lead = lead + (staged.data_ptr(),)
     with torch.cuda.device(dev):
-        rc = fn(xin.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(), off.data_ptr(), E,
-                int(max_rows), y.data_ptr(), N, K, blocksize, tag, _lib.stream_handle(dev))
+        rc = fn(*lead, E, int(max_rows), y.data_ptr(), N, K, blocksize, tag, _lib.stream_handle(dev))
     _lib.check(rc, "stm_nf4_grouped_gemm_" + ("bwd_dx" if backward else "fwd"))
     return y
 

@@ -91,8 +91,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu(L):
     assert L.stm_nf4_gemm_bwd_dx(p, p, p, None, None, 0, p, 4, 40, 64, 64, 1, None, 0, None) == -2
     # misaligned pointer
     assert L.stm_nf4_gemm_fwd(p + 2, p, p, None, None, None, 0, p, 4, 8, 64, 64, 1, None, 0, None) == -1
-    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, None, 4, 16, p, 8, 64, 64, 1, None) == -1
-    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, p, 0, 16, p, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, None, None, 4, 16, p, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_grouped_gemm_fwd(p, p, p, p, None, 0, 16, p, 8, 64, 64, 1, None) == -1
+    assert L.stm_nf4_grouped_tile_rows(None, 4) == -1
+    assert L.stm_nf4_grouped_tile_rows(p, 0) == -1
     assert L.stm_nf4_decision_boundaries(3, p) == -1
 
 
@@ -288,3 +290,22 @@ def test_noalloc_forward_refuses_oversized_problems_before_touching_a_gpu(L):
     assert L.stm_nf4_gemm_fwd_noalloc(p, p, p, None, None, None, 0, p, 16, 4096, 100, 64, 1, None) == -2
     assert L.stm_nf4_gemm_fwd_noalloc(None, p, p, None, None, None, 0, p, 16, 4096, 128, 64, 1, None) == -1
     assert L.stm_nf4_gemm_fwd_noalloc(p, p, p, None, None, None, 8, p, 16, 4096, 128, 64, 1, None) == -1
+
+
+@pytest.mark.parametrize("counts, rows", [
+    # top-8 of 8192 tokens over 128 experts: ~512 rows each, half just above 512.
+    # 256-row tiles compute 64 * 768 + 64 * 512 = 81920 rows, 192-row tiles
+    # 128 * 576 = 73728 (x 1.08 = 79626): the shorter tile
+    ([540] * 64 + [490] * 64, 192),
+    ([512] * 16, 256),          # 8192 rows either way at 256, 9216 * 1.08 at 192
+    ([256] * 8, 256),           # exact 256-row tiles
+    ([100] * 8, 192),           # 192 < 256 padded rows, 207 weighted
+    ([0, 0, 0], 256),           # nothing to compute: the default
+    ([0, 520, 0, 515], 192),    # empty experts skipped: 1536 vs 1152 * 1.08
+    ([700], 256),               # 768 vs 768 * 1.08
+])
+def test_grouped_tile_rows_picks_the_fewest_padded_rows(L, counts, rows):
+    import numpy as np
+    off = np.zeros(len(counts) + 1, dtype=np.int32)
+    off[1:] = np.cumsum(counts)
+    assert L.stm_nf4_grouped_tile_rows(off.ctypes.data, len(counts)) == rows

@@ -205,3 +205,40 @@ def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
             continue
         assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], e
         assert rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype], e
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_forward_picks_192_row_tiles_from_host_counts(cuda, monkeypatch, dtype):
+    """32 experts of 540 or 490 rows (one empty, one of 1 row): 256-row tiles
+    would compute 19456 rows, 192-row tiles 17472 (x 1.08 = 18870), so with
+    enough tiles to fill the GPU the library's own choice is the 192-row
+    register-weight kernel (seen in the profile); its result matches the fp32
+    reference per expert and the forced 256-row kernel."""
+    from stratum_amd import _lib
+    from stratum_amd.functional import nf4_grouped_gemm
+    E, N, K = 32, 1536, 512
+    counts = [540, 490] * 15 + [0, 1]
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    assert _lib.lib().stm_nf4_grouped_tile_rows(off.data_ptr(), E) == 192
+    w = seeded((E, N, K), 91, 0.02, torch.float16)
+    bits = w.reshape(-1, K).contiguous().view(torch.int16).numpy().view(np.uint16)
+    rp, ra = C.quantize(bits, O.DT_F16, 64, "argmin")
+    deq = C.dequantize(rp, ra, E * N * K, 64, TAG[dtype]).view(np.int16).reshape(E, N, K)
+    wq = torch.from_numpy(deq).view(dtype).float().to(cuda)
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    x = seeded((int(off[-1]), K), 92, 1.0, dtype).to(cuda)
+    set_tile(monkeypatch, None)
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        y = nf4_grouped_gemm(x, q, a, off, (N, K), 64)
+        torch.cuda.synchronize()
+    names = [e.key for e in prof.key_averages()]
+    if any("k_gemm" in n for n in names):  # the profiler saw device kernels
+        assert any("k_gemm_fwd_rw" in n and "192" in n for n in names), names
+    set_tile(monkeypatch, "big")
+    y256 = nf4_grouped_gemm(x, q, a, off, (N, K), 64)
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], e
+    assert rel(y, y256) <= TOL[dtype] / 4
