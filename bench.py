@@ -111,6 +111,14 @@ def cpu_baseline(torch, w_half, N, K, sample_rows):
     mm_s = time.perf_counter() - t0
     del y
     flops = 2.0 * sample_rows * N * K
+    # vectorised torch on the same cores: the reference's own CPU formulation
+    tp, ta = torch.from_numpy(packed), torch.from_numpy(absmax)
+    tdeq_s, wt = _timed_loop(lambda: _torch_cpu_dequantize(tp, ta, torch.bfloat16), 3.0)
+    if not torch.equal(wt.view(torch.int16), torch.from_numpy(wd.view(np.int16))):
+        raise RuntimeError("torch CPU dequantize disagrees with the oracle")
+    torch_leg = {"value": round(flops / (tdeq_s + mm_s) / 1e12, 4), "unit": "TFLOP/s",
+                 "what": "vectorised torch dequantize of W (bit-identical to the oracle's) + the same matmul",
+                 "dequant_gbs": round(2.5625 * n / tdeq_s / 1e9, 3)}
     return {
         "value": round(flops / (deq_s + mm_s) / 1e12, 4),
         "unit": "TFLOP/s",
@@ -120,7 +128,46 @@ def cpu_baseline(torch, w_half, N, K, sample_rows):
                    f"rows of X (of 8192)"),
         "dequant_gbs": round(2.5625 * n / deq_s / 1e9, 3),
         "cpu_model": _cpu_model(),
+        "torch_vectorised": torch_leg,
     }
+
+
+def _torch_cpu_quantize(w, blocksize=64, chunk=1 << 20):
+    """bitsandbytes' CPU quantize_4bit restated in vectorised torch (the path
+    the reference runs at staging time, stratum/upload.py:360-369): blockwise
+    absmax, s = x * (1 / absmax) in fp32, the nearest level by argmin (first
+    index on ties), two codes per byte (even element in the high nibble)."""
+    import torch
+    from stratum_amd.functional import NF4_LEVELS
+    code = torch.tensor(NF4_LEVELS, dtype=torch.float32)
+    xf = w.reshape(-1, blocksize).float()
+    absmax = xf.abs().amax(1)
+    s = (xf * (1.0 / absmax).unsqueeze(1)).reshape(-1)
+    codes = torch.empty(s.numel(), dtype=torch.uint8)
+    for i in range(0, s.numel(), chunk):
+        codes[i:i + chunk] = (s[i:i + chunk, None] - code).abs().argmin(1).to(torch.uint8)
+    pairs = codes.view(-1, 2)
+    return (pairs[:, 0] << 4) | pairs[:, 1], absmax
+
+
+def _torch_cpu_dequantize(packed, absmax, dtype, blocksize=64):
+    """bitsandbytes' CPU dequantize_4bit restated in vectorised torch: level *
+    absmax in fp32, one rounding to dtype."""
+    import torch
+    from stratum_amd.functional import NF4_LEVELS
+    code = torch.tensor(NF4_LEVELS, dtype=torch.float32)
+    vals = torch.stack([code[(packed >> 4).long()], code[(packed & 15).long()]], 1).reshape(-1, blocksize)
+    return (vals * absmax.unsqueeze(1)).reshape(-1).to(dtype)
+
+
+def _timed_loop(fn, seconds):
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        out = fn()
+        reps += 1
+        if time.perf_counter() - t0 > seconds:
+            return (time.perf_counter() - t0) / reps, out
 
 
 def _profiled_traffic():
@@ -338,6 +385,13 @@ def run_roundtrip(torch, args):
         cpu_s = (time.perf_counter() - t0) / reps
         res["cpu_roundtrip_ms"] = round(cpu_s * 1e3, 2)
         res["cpu_threads"] = threads
+        torch.set_num_threads(threads)
+        wc = w.cpu()
+        tq_s, (tp, ta) = _timed_loop(lambda: _torch_cpu_quantize(wc), 2.0)
+        td_s, _ = _timed_loop(lambda: _torch_cpu_dequantize(tp, ta, torch.float16), 1.0)
+        if not (np.array_equal(tp.numpy(), p_) and np.array_equal(ta.numpy(), a_)):
+            raise RuntimeError("torch CPU quantize disagrees with the oracle")
+        res["torch_cpu_roundtrip_ms"] = round((tq_s + td_s) * 1e3, 2)
         res["gpu_roundtrip_ms"] = round(q_ms + d_ms, 4)
     return res
 

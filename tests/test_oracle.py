@@ -127,12 +127,43 @@ def test_decision_boundaries_characterise_the_rules():
     np.testing.assert_array_equal(bt, np.nextafter(t, np.float32(2)))
 
 
-def test_rules_agree_on_config1_matrix():
-    x = seeded((5632, 2048), 0, 0.02, torch.float16).numpy().view(np.uint16)
-    pa, aa = C.quantize(x, O.DT_F16, 64, "argmin")
-    pt, at = C.quantize(x, O.DT_F16, 64, "threshold")
+@pytest.mark.parametrize("shape,seed", [
+    ((5632, 2048), 0),     # the round-trip matrix
+    ((14336, 4096), 1),    # 8B gate / up projection, the LoRA-step weight
+    ((4096, 14336), 2),    # 8B down projection
+    ((3072, 1024), 3),     # Qwen3-0.6B gate / up
+    ((16 * 1536, 2048), 4),  # 16 experts of the MoE gate_up bank
+])
+def test_rules_differ_only_at_exact_midpoints_on_the_workload_matrices(shape, seed):
+    """The two published assignment rules (bitsandbytes' torch/CPU argmin and
+    its CUDA threshold tree) on every workload matrix (fp16 N(0, 0.02)): the
+    same absmax, and codes that differ only for elements whose scaled value is
+    exactly an fp32 midpoint between two levels, where the threshold rule takes
+    the lower level. There are a handful of such elements per matrix (one
+    -0.0368042 / 0.060272217 pair of fp16 values lands on the midpoint between
+    levels 1 and 2), not none."""
+    x = seeded(shape, seed, 0.02, torch.float16).numpy().view(np.uint16)
+    threads = min(8, os.cpu_count() or 1)
+    pa, aa = C.quantize(x, O.DT_F16, 64, "argmin", threads)
+    pt, at = C.quantize(x, O.DT_F16, 64, "threshold", threads)
     np.testing.assert_array_equal(aa, at)
-    assert int((pa != pt).sum()) == 0
+    bytes_ = np.nonzero(pa != pt)[0]
+    assert bytes_.size <= 32, bytes_.size
+    if bytes_.size == 0:
+        return
+    elems = np.concatenate([2 * bytes_, 2 * bytes_ + 1])
+    xf = O.to_f32(x.ravel()[elems].view(np.float16), O.DT_F16)
+    s = O.scaled_values(xf, aa[elems // 64], 1)
+    mids = O.midpoint_thresholds()
+    code_a, code_t = O.nearest_codes(s, "argmin"), O.nearest_codes(s, "threshold")
+    differ = code_a != code_t
+    assert differ.any()
+    np.testing.assert_array_equal(np.isin(s[differ], mids), True)
+    np.testing.assert_array_equal(code_t[differ], np.searchsorted(mids, s[differ]))
+    # the packed bytes carry exactly these codes (high nibble = even element)
+    for rule_codes, packed in ((code_a, pa), (code_t, pt)):
+        nib = np.where(elems % 2 == 0, packed[elems // 2] >> 4, packed[elems // 2] & 15)
+        np.testing.assert_array_equal(nib, rule_codes)
 
 
 # ---------------------------------------------------------------- packing
