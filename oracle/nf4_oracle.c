@@ -178,10 +178,20 @@ void nf4o_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int 
 /*
  * Exhaustive check of a cell table of the form used by the product kernels:
  * for every fp32 s in [-1, 1] (and NaN, +-inf, values just outside), the code
- *   c = clamp(s) ; j = (int)(c * 32 + 32) ; code = base[j] + (c >= bound[j])
- * must equal nf4o_code(s, rounding). Returns the number of mismatches and
- * writes the first mismatching bit pattern to *first_bad.
+ *   c = clamp(s) ; f = fma(c, 32, 2^21 + 32) ; j = (bits(f) & 0x3FC) >> 2 ;
+ *   code = base[j] + (c >= bound[j])
+ * must equal nf4o_code(s, rounding). (f lies in [2^21, 2^22), where the float
+ * spacing is 1/4, so bits(f) & 0x3FC is 4 * floor(round(128 c + 128) / 4).)
+ * Returns the number of mismatches and writes the first mismatching bit
+ * pattern to *first_bad.
  */
+static int cell_index(float c) {
+    float f = fmaf(c, 32.0f, 2097184.0f);
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return (int)((u & 0x3FCu) >> 2);
+}
+
 int64_t nf4o_check_cells(const float* bound, const uint8_t* base, int ncell, int rounding, uint32_t* first_bad) {
     int64_t bad = 0;
     uint32_t first = 0;
@@ -195,7 +205,7 @@ int64_t nf4o_check_cells(const float* bound, const uint8_t* base, int ncell, int
             float s;
             memcpy(&s, &u, 4);
             float c = s != s ? -1.0f : (s < -1.0f ? -1.0f : (s > 1.0f ? 1.0f : s));
-            int j = (int)(c * 32.0f + 32.0f);
+            int j = cell_index(c);
             if (j < 0 || j >= ncell) {
                 bad++;
                 continue;
@@ -218,7 +228,7 @@ int64_t nf4o_check_cells(const float* bound, const uint8_t* base, int ncell, int
         float s;
         memcpy(&s, &specials[t], 4);
         float c = s != s ? -1.0f : (s < -1.0f ? -1.0f : (s > 1.0f ? 1.0f : s));
-        int j = (int)(c * 32.0f + 32.0f);
+        int j = cell_index(c);
         int got = base[j] + (c >= bound[j] ? 1 : 0);
         if (got != nf4o_code(s, rounding)) bad++;
     }

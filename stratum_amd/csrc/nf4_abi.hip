@@ -73,8 +73,11 @@ int build_cell_table(int rounding, CellTable* tab) {
     int rc = decision_boundaries(rounding, b);
     if (rc) return rc;
     for (int j = 0; j <= 64; ++j) {
-        // s values that can land in cell j, widened by 1/64 of a cell on both sides
-        double lo = (j - 1.0 / 64) / 32.0 - 1.0, hi = (j + 1.0 + 1.0 / 64) / 32.0 - 1.0;
+        // s values that can land in cell j -- round(128 c + 128) in [4 j, 4 j + 3],
+        // i.e. c in [(4 j - 0.5) / 128 - 1, (4 j + 3.5) / 128 - 1] -- widened to a
+        // quarter cell on both sides; a boundary in the margin is still exact
+        // (every c of the cell is then on one side of it)
+        double lo = (j - 0.25) / 32.0 - 1.0, hi = (j + 1.25) / 32.0 - 1.0;
         uint32_t base = 0;
         int inside = 0;
         float bound = 2.0f;  // never reached: clamped s <= 1

@@ -25,17 +25,19 @@ using Tr16 = std::conditional_t<DT == STM_BF16, BF16, F16>;
 __device__ __forceinline__ float nanmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // Level of s = x / absmax. s is clamped to [-1, 1] (v_med3_f32: +-inf from an
-// absmax whose reciprocal overflows go to +-1, as the CPU rule's clamp does);
-// cell j = (int)(c * 32 + 32) in [0, 64] (c * 32 is exact, so the fma rounds
-// once, like the multiply-then-add the table was built for), converted with
-// v_cvt_i32_f32, which maps NaN to 0. A NaN s (all-zero or NaN block) thus
-// reaches cell 0, whose base is code 0 and whose bound (2.0) is never met --
-// code 0, as both bitsandbytes rules give -- whether v_med3 returns the NaN or -1.
+// absmax whose reciprocal overflows go to +-1, as the CPU rule's clamp does).
+// The cell index comes from the bits of f = c * 32 + (2^21 + 32) (one
+// rounding; c * 32 is exact): in [2^21, 2^22) the float spacing is 1/4, so the
+// low mantissa bits of f hold round(128 c + 128) in [0, 256], and those bits &
+// 0x3FC are 4 * cell (cell in [0, 64]) -- already the byte offset of the
+// cell's entry, with no convert or shift. A NaN s (all-zero or NaN block)
+// gives f = NaN whose bits & 0x3FC are 0, and c = -1 gives f = 2^21, also
+// cell 0, whose base is code 0 and whose bound (2.0) is never met -- code 0,
+// as both bitsandbytes rules give, whether v_med3 returns the NaN or -1.
 __device__ __forceinline__ uint32_t level_of(float s, const float* __restrict__ bound,
                                              const uint32_t* __restrict__ base) {
     const float c = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
-    int j;
-    __asm__("v_cvt_i32_f32 %0, %1" : "=v"(j) : "v"(__builtin_fmaf(c, 32.0f, 32.0f)));
+    const uint32_t j = (__float_as_uint(__builtin_fmaf(c, 32.0f, 2097184.0f)) & 0x3FCu) >> 2;
     return base[j] + (c >= bound[j] ? 1u : 0u);
 }
 
@@ -47,22 +49,92 @@ __device__ __forceinline__ float load1(const void* x, int64_t i) {
         return Tr16<DT>::to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
 }
 
-// elements 8g .. 8g+7
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// fp32(half h of w) * r, one rounding: v_fma_mix_f32 with a zero addend (the
+// conversion of the fp16 operand is exact), one VALU op for convert + scale.
+template <int HI>
+__device__ __forceinline__ float f16_times(uint32_t w, float r) {
+    float s;
+    if constexpr (HI)
+        __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(s) : "v"(w), "v"(r));
+    else
+        __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(s) : "v"(w), "v"(r));
+    return s;
+}
+// per-half IEEE maximum of three packed fp16 pairs (NaN-propagating)
+__device__ __forceinline__ uint32_t pk_max3_f16(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    __asm__("v_pk_maximum3_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+#pragma clang diagnostic pop
+
+// One lane's 8 elements of a chunk: 16-bit inputs stay packed (4 words),
+// fp32 inputs are 8 floats.
 template <int DT>
-__device__ __forceinline__ void load8(const void* __restrict__ x, int64_t g, float* v) {
-    if constexpr (DT == STM_F32) {
+struct Chunk8 {
+    uint4 w;
+    __device__ __forceinline__ void load(const void* __restrict__ x, int64_t g) {
+        w = reinterpret_cast<const uint4*>(x)[g];
+    }
+    __device__ __forceinline__ void zero() { w = make_uint4(0u, 0u, 0u, 0u); }
+    __device__ __forceinline__ uint32_t word(int k) const { return k == 0 ? w.x : k == 1 ? w.y : k == 2 ? w.z : w.w; }
+    // element 2k + h scaled by r, in fp32 (one rounding)
+    __device__ __forceinline__ float scaled(int k, int h, float r) const {
+        if constexpr (DT == STM_F16)
+            return h ? f16_times<1>(word(k), r) : f16_times<0>(word(k), r);
+        else
+            return (h ? __uint_as_float(word(k) & 0xFFFF0000u) : __uint_as_float(word(k) << 16)) * r;
+    }
+};
+template <>
+struct Chunk8<STM_F32> {
+    float v[8];
+    __device__ __forceinline__ void load(const void* __restrict__ x, int64_t g) {
         const float4* p = reinterpret_cast<const float4*>(x) + 2 * g;
-        float4 a = p[0], b = p[1];
+        const float4 a = p[0], b = p[1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-        uint4 w = reinterpret_cast<const uint4*>(x)[g];
-        uint32_t u[4] = {w.x, w.y, w.z, w.w};
+    }
+    __device__ __forceinline__ void zero() {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            v[2 * k] = Tr16<DT>::to_f32((uint16_t)(u[k] & 0xFFFFu));
-            v[2 * k + 1] = Tr16<DT>::to_f32((uint16_t)(u[k] >> 16));
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    }
+    __device__ __forceinline__ float scaled(int k, int h, float r) const { return v[2 * k + h] * r; }
+};
+
+// max|x| over a lane's C chunks, in fp32 (NaN-propagating). fp16: per-half
+// maxima of |x| on the packed words (v_pk_maximum3_f16 on x & 0x7FFF7FFF),
+// then the two halves, then one exact conversion; the others in fp32.
+template <int DT, int C>
+__device__ __forceinline__ float lane_absmax(const Chunk8<DT> (&ch)[C]) {
+    if constexpr (DT == STM_F16) {
+        uint32_t m = ch[0].w.x & 0x7FFF7FFFu;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const uint32_t a = ch[c].w.x & 0x7FFF7FFFu, b = ch[c].w.y & 0x7FFF7FFFu;
+            const uint32_t d = ch[c].w.z & 0x7FFF7FFFu, e = ch[c].w.w & 0x7FFF7FFFu;
+            m = pk_max3_f16(pk_max3_f16(m, a, b), d, e);
         }
+        m = pk_max3_f16(m, m >> 16, m);  // low half: max of both halves (the high half of m >> 16 is +0)
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)(m & 0xFFFFu));
+    } else if constexpr (DT == STM_BF16) {
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a = nanmax(nanmax(a, fabsf(__uint_as_float(ch[c].word(k) << 16))),
+                           fabsf(__uint_as_float(ch[c].word(k) & 0xFFFF0000u)));
+        return a;
+    } else {
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = nanmax(a, fabsf(ch[c].v[e]));
+        return a;
     }
 }
 
@@ -70,11 +142,15 @@ __device__ __forceinline__ void load8(const void* __restrict__ x, int64_t g, flo
 // A wave handles U rounds of 64 / L consecutive blocks. All its loads are
 // issued first (U * C 16-byte loads per lane in flight), then the cell table
 // is copied to LDS -- so the table setup and the barrier overlap the HBM
-// latency -- and then each round is reduced, quantized and stored. Every
-// thread reaches the barrier; rounds past the end are masked.
+// latency. The U rounds' absmax values are reduced first; lane u of each
+// block's L lanes then computes the reciprocal for round u (one IEEE division
+// per lane instead of U), which the group's lanes read back with a shuffle.
+// Then each round is quantized and stored. Every thread reaches the barrier;
+// rounds past the end are masked.
 template <int DT, int L, int C, int U>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
                                                   float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
+    static_assert(U <= L, "one reciprocal per lane of a block's group");
     __shared__ float s_bound[65];
     __shared__ uint32_t s_base[65];
     constexpr int BPW = 64 / L;  // blocks per round
@@ -83,18 +159,16 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, ui
     const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
     const int64_t first = wave * (BPW * U);
 
-    float v[U][C][8];
+    Chunk8<DT> ch[U][C];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t blk = first + u * BPW + lane / L;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            if (blk < nblocks) {
-                load8<DT>(x, blk * GPB + c * L + (lane % L), v[u][c]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[u][c][e] = 0.0f;
-            }
+            if (blk < nblocks)
+                ch[u][c].load(x, blk * GPB + c * L + (lane % L));
+            else
+                ch[u][c].zero();
         }
     }
     if (threadIdx.x < 65) {
@@ -103,30 +177,43 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, ui
     }
     __syncthreads();
 
+    float a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        a[u] = lane_absmax<DT, C>(ch[u]);
+#pragma unroll
+        for (int off = 1; off < L; off <<= 1) a[u] = nanmax(a[u], __shfl_xor(a[u], off));
+    }
+    float r[U];
+    if constexpr (U == 1) {
+        r[0] = 1.0f / a[0];  // IEEE division (correctly rounded)
+    } else {
+        const int k = lane % L;
+        float mine = a[0];
+#pragma unroll
+        for (int u = 1; u < U; ++u) mine = k == u ? a[u] : mine;
+        const float inv = 1.0f / mine;  // IEEE division (correctly rounded), round k's for lanes k < U
+        const int group = lane & ~(L - 1);
+#pragma unroll
+        for (int u = 0; u < U; ++u) r[u] = __shfl(inv, group + u);
+    }
+
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t blk = first + u * BPW + lane / L;
         const bool active = blk < nblocks;
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a = nanmax(a, fabsf(v[u][c][e]));
-#pragma unroll
-        for (int off = 1; off < L; off <<= 1) a = nanmax(a, __shfl_xor(a, off));
-        const float r = 1.0f / a;  // IEEE division (correctly rounded)
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             uint32_t word = 0;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                uint32_t q0 = level_of(v[u][c][2 * p] * r, s_bound, s_base);
-                uint32_t q1 = level_of(v[u][c][2 * p + 1] * r, s_bound, s_base);
+                const uint32_t q0 = level_of(ch[u][c].scaled(p, 0, r[u]), s_bound, s_base);
+                const uint32_t q1 = level_of(ch[u][c].scaled(p, 1, r[u]), s_bound, s_base);
                 word |= ((q0 << 4) | q1) << (8 * p);
             }
             if (active) packed[blk * GPB + c * L + (lane % L)] = word;
         }
-        if (active && (lane % L) == 0) absmax[blk] = a;
+        if (active && (lane % L) == 0) absmax[blk] = a[u];
     }
 }
 
