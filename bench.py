@@ -370,7 +370,8 @@ def run_roundtrip(torch, args):
     res = {"shape": [5632, 2048], "quantize_gbs": round(byt / q_ms / 1e6, 1), "quantize_us": round(q_ms * 1e3, 2),
            "dequantize_gbs": round(byt / d_ms / 1e6, 1), "dequantize_us": round(d_ms * 1e3, 2),
            "timing": "device time: 50 launches captured in one HIP graph, replayed",
-           "quantize_call_us_from_python": round(q_call_ms * 1e3, 2)}
+           "quantize_call_us_from_python": round(q_call_ms * 1e3, 2),
+           "aggregate": _roundtrip_aggregate(torch, dev)}
     if not args.no_cpu:
         from oracle import c_oracle as C
         from oracle import nf4_oracle as O
@@ -394,6 +395,36 @@ def run_roundtrip(torch, args):
         res["torch_cpu_roundtrip_ms"] = round((tq_s + td_s) * 1e3, 2)
         res["gpu_roundtrip_ms"] = round(q_ms + d_ms, 4)
     return res
+
+
+def _roundtrip_aggregate(torch, dev):
+    """The matrices of one TinyLlama-1.1B decoder layer (q/o [2048,2048], k/v
+    [256,2048], gate/up [5632,2048], down [2048,5632]; fp16 N(0, 0.02)) quantized
+    and dequantized in one batched launch each, against one launch per matrix."""
+    from stratum_amd.functional import dequantize_4bit, dequantize_4bit_many, quantize_4bit, quantize_4bit_many
+    shapes = [(2048, 2048), (256, 2048), (256, 2048), (2048, 2048), (5632, 2048), (5632, 2048), (2048, 5632)]
+    ws = [seeded(torch, sh, 60 + i, 0.02, torch.float16, dev) for i, sh in enumerate(shapes)]
+    qs = quantize_4bit_many(ws)
+    outs = [torch.empty_like(w) for w in ws]
+    n = sum(w.numel() for w in ws)
+    byt = 2.5625 * n
+
+    def per_matrix_q():
+        for w in ws:
+            quantize_4bit(w)
+
+    def per_matrix_d():
+        for (p, st), o in zip(qs, outs):
+            dequantize_4bit(p, st, out=o)
+
+    qm = graph_time_ms(torch, lambda: quantize_4bit_many(ws), 20)
+    dm = graph_time_ms(torch, lambda: dequantize_4bit_many(qs, out=outs), 20)
+    q1 = graph_time_ms(torch, per_matrix_q, 20)
+    d1 = graph_time_ms(torch, per_matrix_d, 20)
+    return {"tensors": len(ws), "elements": n,
+            "quantize_many_us": round(qm * 1e3, 2), "quantize_many_gbs": round(byt / qm / 1e6, 1),
+            "dequantize_many_us": round(dm * 1e3, 2), "dequantize_many_gbs": round(byt / dm / 1e6, 1),
+            "one_launch_per_matrix": {"quantize_us": round(q1 * 1e3, 2), "dequantize_us": round(d1 * 1e3, 2)}}
 
 
 def run_qwen06(torch, args):

@@ -78,6 +78,21 @@ int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, in
                        int out_dtype, void* stream);
 
 /*
+ * Many tensors per call: stm_nf4_quantize / stm_nf4_dequantize applied to
+ * tensors t = 0 .. count-1 (host arrays of device pointers and sizes; one
+ * dtype, blocksize and rule for all), with the whole blocks of up to 32
+ * tensors in one launch. Same results, bit for bit, as one call per tensor.
+ * Batches the per-parameter loops of stratum/upload.py prepare_nf4
+ * (:305-398, quantize) and ensure_weights / NF4Prefetch.finalize (:969-1069,
+ * :187-225, dequantize), which call bitsandbytes once per parameter; a
+ * layer's projections then cost one launch instead of one each.
+ */
+int stm_nf4_quantize_many(int count, const void* const* A, const int64_t* n, int dtype, int blocksize, int rounding,
+                          uint8_t* const* packed, float* const* absmax, void* stream);
+int stm_nf4_dequantize_many(int count, const uint8_t* const* packed, const float* const* absmax, const int64_t* n,
+                            int blocksize, void* const* out, int out_dtype, void* stream);
+
+/*
  * Fused NF4 dequant-GEMM, forward of a frozen Linear:
  *   Y[M, N] = X[M, K] . W[N, K]^T  (+ bias[N])  (+ T[M, R] . L[N, R]^T)
  * with W given as NF4 (packed [N*K/2], absmax [N*K/blocksize]) and dequantized

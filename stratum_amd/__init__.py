@@ -6,8 +6,8 @@ and ``stratum/nf4_linear.py``); the NF4 arithmetic runs in the HIP library
 ``libstratum_nf4.so`` (C ABI: ``include/stratum_nf4.h``).
 """
 
-from .functional import (QuantState, dequantize_4bit, get_4bit_type, nf4_gemm_bwd_dx, nf4_gemm_fwd,
-                         nf4_grouped_gemm, quantize_4bit)
+from .functional import (QuantState, dequantize_4bit, dequantize_4bit_many, get_4bit_type, nf4_gemm_bwd_dx,
+                         nf4_gemm_fwd, nf4_grouped_gemm, quantize_4bit, quantize_4bit_many)
 from .nf4_linear import NF4Linear, NF4LoRALinear, nf4_linear
 from .upload import (FP16_ATTR, NF4_ATTR, FP16StagedPayload, NF4Payload, NF4Prefetch, NF4Stats,
                      ensure_prefetched_weights, ensure_weights, estimate_module_upload_gib, free_weights,
@@ -15,8 +15,8 @@ from .upload import (FP16_ATTR, NF4_ATTR, FP16StagedPayload, NF4Payload, NF4Pref
                      quantize_and_attach, restore_module_buffers, snapshot_module_buffers, upload_stream)
 
 __all__ = [
-    "QuantState", "dequantize_4bit", "get_4bit_type", "quantize_4bit", "nf4_gemm_fwd", "nf4_gemm_bwd_dx",
-    "nf4_grouped_gemm", "NF4Linear", "NF4LoRALinear", "nf4_linear", "FP16_ATTR", "NF4_ATTR",
+    "QuantState", "dequantize_4bit", "dequantize_4bit_many", "get_4bit_type", "quantize_4bit",
+    "quantize_4bit_many", "nf4_gemm_fwd", "nf4_gemm_bwd_dx", "nf4_grouped_gemm", "NF4Linear", "NF4LoRALinear", "nf4_linear", "FP16_ATTR", "NF4_ATTR",
     "FP16StagedPayload", "NF4Payload", "NF4Prefetch", "NF4Stats", "ensure_prefetched_weights", "ensure_weights",
     "estimate_module_upload_gib", "free_weights", "prefetch_weights", "prepare_fp16_staged", "prepare_nf4",
     "prepare_nf4_from_cache", "quantize_and_attach", "restore_module_buffers", "snapshot_module_buffers",

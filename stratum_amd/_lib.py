@@ -43,6 +43,8 @@ SIGNATURES = {
     "stm_nf4_gemm_set_tile": ([_I], _I),
     "stm_nf4_grouped_gemm_fwd": ([_P, _P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
     "stm_nf4_grouped_tile_rows": ([_P, _I], _I),
+    "stm_nf4_quantize_many": ([_I, _P, _P, _I, _I, _I, _P, _P, _P], _I),
+    "stm_nf4_dequantize_many": ([_I, _P, _P, _P, _I, _P, _I, _P], _I),
     "stm_nf4_grouped_gemm_bwd_dx": ([_P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
     "stm_swiglu_fwd": ([_P, _P, _I64, _I64, _I, _P], _I),
     "stm_swiglu_bwd": ([_P, _P, _P, _I64, _I64, _I, _P], _I),

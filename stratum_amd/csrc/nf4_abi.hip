@@ -204,6 +204,45 @@ int stm_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, in
     return launch_dequantize(packed, absmax, n, blocksize, out, out_dtype, (hipStream_t)stream);
 }
 
+int stm_nf4_quantize_many(int count, const void* const* A, const int64_t* n, int dtype, int blocksize, int rounding,
+                          uint8_t* const* packed, float* const* absmax, void* stream) {
+    g_err[0] = 0;
+    if (count < 0) return set_error(STM_ERR_INVALID, "quantize_many: count %d < 0", count);
+    if (!valid_dtype(dtype)) return set_error(STM_ERR_INVALID, "quantize_many: bad dtype %d", dtype);
+    if (!valid_blocksize(blocksize))
+        return set_error(STM_ERR_INVALID, "quantize_many: blocksize %d not a power of two in [64, 4096]", blocksize);
+    const CellTable* tab = cell_table(rounding);
+    if (!tab) return set_error(STM_ERR_INVALID, "quantize_many: unknown rounding rule %d", rounding);
+    if (count == 0) return STM_OK;
+    if (!A || !n || !packed || !absmax) return set_error(STM_ERR_INVALID, "quantize_many: NULL array");
+    for (int t = 0; t < count; ++t) {
+        if (n[t] < 0) return set_error(STM_ERR_INVALID, "quantize_many: n[%d] = %lld < 0", t, (long long)n[t]);
+        if (n[t] > 0 && (!A[t] || !packed[t] || !absmax[t]))
+            return set_error(STM_ERR_INVALID, "quantize_many: NULL pointer for tensor %d", t);
+        if ((n[t] + 3) / 4 > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "quantize_many: n[%d] too large", t);
+    }
+    return launch_quantize_many(count, A, n, dtype, blocksize, *tab, packed, absmax, (hipStream_t)stream);
+}
+
+int stm_nf4_dequantize_many(int count, const uint8_t* const* packed, const float* const* absmax, const int64_t* n,
+                            int blocksize, void* const* out, int out_dtype, void* stream) {
+    g_err[0] = 0;
+    if (count < 0) return set_error(STM_ERR_INVALID, "dequantize_many: count %d < 0", count);
+    if (!valid_dtype(out_dtype)) return set_error(STM_ERR_INVALID, "dequantize_many: bad dtype %d", out_dtype);
+    if (!valid_blocksize(blocksize))
+        return set_error(STM_ERR_INVALID, "dequantize_many: blocksize %d not a power of two in [64, 4096]", blocksize);
+    if (count == 0) return STM_OK;
+    if (!packed || !absmax || !n || !out) return set_error(STM_ERR_INVALID, "dequantize_many: NULL array");
+    for (int t = 0; t < count; ++t) {
+        if (n[t] < 0) return set_error(STM_ERR_INVALID, "dequantize_many: n[%d] = %lld < 0", t, (long long)n[t]);
+        if (n[t] > 0 && (!packed[t] || !absmax[t] || !out[t]))
+            return set_error(STM_ERR_INVALID, "dequantize_many: NULL pointer for tensor %d", t);
+        if ((n[t] + 255) / 256 > 0x7FFFFFFFLL)
+            return set_error(STM_ERR_UNSUPPORTED, "dequantize_many: n[%d] too large", t);
+    }
+    return launch_dequantize_many(count, packed, absmax, n, blocksize, out, out_dtype, (hipStream_t)stream);
+}
+
 static int check_gemm_common(const char* who, const void* a, const uint8_t* packed, const float* absmax,
                              const void* out, int64_t M, int64_t N, int64_t K, int blocksize, int dtype) {
     if (!is_16bit(dtype)) return set_error(STM_ERR_INVALID, "%s: dtype %d is not bf16/fp16", who, dtype);

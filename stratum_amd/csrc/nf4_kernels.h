@@ -55,6 +55,12 @@ int launch_quantize(const void* A, int dtype, int64_t n, int blocksize, const Ce
                     float* absmax, hipStream_t stream);
 int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int blocksize, void* out, int out_dtype,
                       hipStream_t stream);
+// Many tensors of one dtype / blocksize (/ rule): batched launches of whole
+// blocks, per-tensor launches for partial blocks and unaligned tensors.
+int launch_quantize_many(int count, const void* const* A, const int64_t* n, int dtype, int bs, const CellTable& tab,
+                         uint8_t* const* packed, float* const* absmax, hipStream_t stream);
+int launch_dequantize_many(int count, const uint8_t* const* packed, const float* const* absmax, const int64_t* n,
+                           int bs, void* const* out, int out_dtype, hipStream_t stream);
 int launch_gemm_fwd(const GemmArgs& g, int dtype, hipStream_t stream);
 int launch_gemm_bwd(const GemmArgs& g, int dtype, hipStream_t stream);
 

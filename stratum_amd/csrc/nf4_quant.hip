@@ -16,6 +16,10 @@ namespace stm {
 
 #pragma clang fp contract(off)
 
+// Tensors per batched (de)quantize launch; their pointers and sizes travel as
+// kernel arguments (under 2 KB).
+constexpr int kManyMax = 32;
+
 template <int DT>
 using Tr16 = std::conditional_t<DT == STM_BF16, BF16, F16>;
 
@@ -148,15 +152,14 @@ __device__ __forceinline__ float lane_absmax(const Chunk8<DT> (&ch)[C]) {
 // Then each round is quantized and stored. Every thread reaches the barrier;
 // rounds past the end are masked.
 template <int DT, int L, int C, int U>
-__global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
-                                                  float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
+__device__ __forceinline__ void quantize_workgroup(const void* __restrict__ x, uint32_t* __restrict__ packed,
+                                                   float* __restrict__ absmax, int64_t nblocks, int64_t wg,
+                                                   const CellTable& tab, float* s_bound, uint32_t* s_base) {
     static_assert(U <= L, "one reciprocal per lane of a block's group");
-    __shared__ float s_bound[65];
-    __shared__ uint32_t s_base[65];
     constexpr int BPW = 64 / L;  // blocks per round
     constexpr int GPB = L * C;   // 8-element groups per block
     const int lane = threadIdx.x & 63;
-    const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+    const int64_t wave = (wg * 256 + threadIdx.x) >> 6;
     const int64_t first = wave * (BPW * U);
 
     Chunk8<DT> ch[U][C];
@@ -217,6 +220,42 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, ui
     }
 }
 
+template <int DT, int L, int C, int U>
+__global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
+                                                  float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
+    __shared__ float s_bound[65];
+    __shared__ uint32_t s_base[65];
+    quantize_workgroup<DT, L, C, U>(x, packed, absmax, nblocks, blockIdx.x, tab, s_bound, s_base);
+}
+
+// Several tensors in one launch (the same dtype, blocksize and rule): tensor t
+// owns work-groups [first_wg[t], first_wg[t + 1]); each work-group finds its
+// tensor with a uniform scan of the (kernel-argument) prefix array.
+struct QuantMany {
+    CellTable tab;
+    int count;
+    int64_t first_wg[kManyMax + 1];
+    const void* x[kManyMax];
+    uint32_t* packed[kManyMax];
+    float* absmax[kManyMax];
+    int64_t nblocks[kManyMax];
+};
+
+__device__ __forceinline__ int tensor_of(const int64_t* first_wg, int count, int64_t wg) {
+    int t = 0;
+    for (int i = 1; i < count; ++i) t += wg >= first_wg[i] ? 1 : 0;
+    return t;
+}
+
+template <int DT, int L, int C, int U>
+__global__ __launch_bounds__(256) void k_quantize_many(QuantMany m) {
+    __shared__ float s_bound[65];
+    __shared__ uint32_t s_base[65];
+    const int t = tensor_of(m.first_wg, m.count, blockIdx.x);
+    quantize_workgroup<DT, L, C, U>(m.x[t], m.packed[t], m.absmax[t], m.nblocks[t], blockIdx.x - m.first_wg[t], m.tab,
+                                    s_bound, s_base);
+}
+
 // One thread per block; used for a partial last block and for unaligned inputs.
 template <int DT>
 __global__ __launch_bounds__(64) void k_quantize_generic(const void* __restrict__ x, int64_t n, int bs,
@@ -251,6 +290,34 @@ static void quantize_launch(const void* A, int64_t nfull, const CellTable& tab, 
     const int64_t grid = (waves + 3) / 4;
     hipLaunchKernelGGL((k_quantize<DT, L, C, U>), dim3((unsigned)grid), dim3(256), 0, stream, A, p4, absmax, nfull,
                        tab);
+}
+
+template <int DT, int L, int C, int U>
+static int64_t quantize_workgroups(int64_t nfull) {
+    const int64_t per_wave = (64 / L) * U;
+    return ((nfull + per_wave - 1) / per_wave + 3) / 4;
+}
+
+template <int DT, int L, int C, int U>
+static void quantize_many_launch(QuantMany& m, hipStream_t stream) {
+    m.first_wg[0] = 0;
+    for (int t = 0; t < m.count; ++t) m.first_wg[t + 1] = m.first_wg[t] + quantize_workgroups<DT, L, C, U>(m.nblocks[t]);
+    if (m.first_wg[m.count] > 0)
+        hipLaunchKernelGGL((k_quantize_many<DT, L, C, U>), dim3((unsigned)m.first_wg[m.count]), dim3(256), 0, stream,
+                           m);
+}
+
+template <int DT>
+static void quantize_many_dispatch(QuantMany& m, int bs, hipStream_t stream) {
+    switch (bs) {
+        case 64: quantize_many_launch<DT, 8, 1, 4>(m, stream); break;
+        case 128: quantize_many_launch<DT, 16, 1, 4>(m, stream); break;
+        case 256: quantize_many_launch<DT, 32, 1, 4>(m, stream); break;
+        case 512: quantize_many_launch<DT, 64, 1, 4>(m, stream); break;
+        case 1024: quantize_many_launch<DT, 64, 2, 2>(m, stream); break;
+        case 2048: quantize_many_launch<DT, 64, 4, 1>(m, stream); break;
+        default: quantize_many_launch<DT, 64, 8, 1>(m, stream); break;
+    }
 }
 
 template <int DT>
@@ -300,6 +367,63 @@ int launch_quantize(const void* A, int dtype, int64_t n, int bs, const CellTable
     return STM_OK;
 }
 
+int launch_quantize_many(int count, const void* const* A, const int64_t* n, int dtype, int bs, const CellTable& tab,
+                         uint8_t* const* packed, float* const* absmax, hipStream_t stream) {
+    // the whole blocks of 16-byte aligned inputs go through batched launches of
+    // up to kManyMax tensors; partial last blocks and unaligned inputs take
+    // the single-tensor path (its tail kernel)
+    QuantMany m{};
+    m.tab = tab;
+    auto flush = [&]() -> int {
+        if (m.count == 0) return STM_OK;
+        if (dtype == STM_F16)
+            quantize_many_dispatch<STM_F16>(m, bs, stream);
+        else if (dtype == STM_BF16)
+            quantize_many_dispatch<STM_BF16>(m, bs, stream);
+        else
+            quantize_many_dispatch<STM_F32>(m, bs, stream);
+        m.count = 0;
+        return check_launch("quantize_many");
+    };
+    for (int t = 0; t < count; ++t) {
+        const int64_t nfull = (aligned(A[t], 16) && aligned(packed[t], 4)) ? n[t] / bs : 0;
+        if (nfull > 0) {
+            m.x[m.count] = A[t];
+            m.packed[m.count] = reinterpret_cast<uint32_t*>(packed[t]);
+            m.absmax[m.count] = absmax[t];
+            m.nblocks[m.count] = nfull;
+            if (++m.count == kManyMax) {
+                const int rc = flush();
+                if (rc) return rc;
+            }
+        }
+    }
+    int rc = flush();
+    if (rc) return rc;
+    for (int t = 0; t < count; ++t) {
+        const int64_t nfull = (aligned(A[t], 16) && aligned(packed[t], 4)) ? n[t] / bs : 0;
+        const int64_t nblocks = (n[t] + bs - 1) / bs;
+        if (nfull == nblocks) continue;
+        if (nfull == 0) {
+            rc = launch_quantize(A[t], dtype, n[t], bs, tab, packed[t], absmax[t], stream);
+        } else {
+            dim3 g((unsigned)((nblocks - nfull + 63) / 64)), b(64);
+            if (dtype == STM_F16)
+                hipLaunchKernelGGL(k_quantize_generic<STM_F16>, g, b, 0, stream, A[t], n[t], bs, nfull, nblocks,
+                                   packed[t], absmax[t], tab);
+            else if (dtype == STM_BF16)
+                hipLaunchKernelGGL(k_quantize_generic<STM_BF16>, g, b, 0, stream, A[t], n[t], bs, nfull, nblocks,
+                                   packed[t], absmax[t], tab);
+            else
+                hipLaunchKernelGGL(k_quantize_generic<STM_F32>, g, b, 0, stream, A[t], n[t], bs, nfull, nblocks,
+                                   packed[t], absmax[t], tab);
+            rc = check_launch("quantize_many(tail)");
+        }
+        if (rc) return rc;
+    }
+    return STM_OK;
+}
+
 // ------------------------------------------------------------------ dequant
 template <int DT>
 __device__ __forceinline__ void store8(void* __restrict__ out, int64_t g, const float* v) {
@@ -317,14 +441,14 @@ __device__ __forceinline__ void store8(void* __restrict__ out, int64_t g, const 
     }
 }
 
-// U words of packed codes per lane, wave-contiguous: word g = (block*U + j)*256 + tid.
+// U words of packed codes per lane, wave-contiguous: word g = (wg*U + j)*256 + tid.
 template <int DT, int U>
-__global__ __launch_bounds__(256) void k_dequantize(const uint32_t* __restrict__ q, const float* __restrict__ absmax,
-                                                    void* __restrict__ out, int64_t ngroups, int gshift) {
-    __shared__ float2 lut[256];
+__device__ __forceinline__ void dequantize_workgroup(const uint32_t* __restrict__ q, const float* __restrict__ absmax,
+                                                     void* __restrict__ out, int64_t ngroups, int gshift, int64_t wg,
+                                                     float2* lut) {
     lut[threadIdx.x] = make_float2(kLevelsDev[threadIdx.x >> 4], kLevelsDev[threadIdx.x & 15]);
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * (U * 256) + threadIdx.x;
+    const int64_t base = wg * (U * 256) + threadIdx.x;
     uint32_t w[U];
     float a[U];
 #pragma unroll
@@ -351,6 +475,32 @@ __global__ __launch_bounds__(256) void k_dequantize(const uint32_t* __restrict__
             store8<DT>(out, g, v);
         }
     }
+}
+
+template <int DT, int U>
+__global__ __launch_bounds__(256) void k_dequantize(const uint32_t* __restrict__ q, const float* __restrict__ absmax,
+                                                    void* __restrict__ out, int64_t ngroups, int gshift) {
+    __shared__ float2 lut[256];
+    dequantize_workgroup<DT, U>(q, absmax, out, ngroups, gshift, blockIdx.x, lut);
+}
+
+// Several tensors in one launch (the same blocksize and output dtype), as QuantMany.
+struct DequantMany {
+    int count;
+    int gshift;
+    int64_t first_wg[kManyMax + 1];
+    const uint32_t* q[kManyMax];
+    const float* absmax[kManyMax];
+    void* out[kManyMax];
+    int64_t ngroups[kManyMax];
+};
+
+template <int DT, int U>
+__global__ __launch_bounds__(256) void k_dequantize_many(DequantMany m) {
+    __shared__ float2 lut[256];
+    const int t = tensor_of(m.first_wg, m.count, blockIdx.x);
+    dequantize_workgroup<DT, U>(m.q[t], m.absmax[t], m.out[t], m.ngroups[t], m.gshift, blockIdx.x - m.first_wg[t],
+                                lut);
 }
 
 template <int DT>
@@ -397,6 +547,64 @@ int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int
     else
         dequant_dispatch<STM_F32>(packed, absmax, n, bshift, out, vec_ok, stream);
     return check_launch("dequantize");
+}
+
+template <int DT>
+static void dequant_many_launch(DequantMany& m, hipStream_t stream) {
+    constexpr int U = 4;
+    m.first_wg[0] = 0;
+    for (int t = 0; t < m.count; ++t) m.first_wg[t + 1] = m.first_wg[t] + (m.ngroups[t] + U * 256 - 1) / (U * 256);
+    if (m.first_wg[m.count] > 0)
+        hipLaunchKernelGGL((k_dequantize_many<DT, U>), dim3((unsigned)m.first_wg[m.count]), dim3(256), 0, stream, m);
+}
+
+int launch_dequantize_many(int count, const uint8_t* const* packed, const float* const* absmax, const int64_t* n,
+                           int bs, void* const* out, int out_dtype, hipStream_t stream) {
+    // whole 8-element groups of aligned tensors batched, the rest per tensor
+    const int bshift = ilog2(bs);
+    DequantMany m{};
+    m.gshift = bshift - 3;
+    auto flush = [&]() -> int {
+        if (m.count == 0) return STM_OK;
+        if (out_dtype == STM_F16)
+            dequant_many_launch<STM_F16>(m, stream);
+        else if (out_dtype == STM_BF16)
+            dequant_many_launch<STM_BF16>(m, stream);
+        else
+            dequant_many_launch<STM_F32>(m, stream);
+        m.count = 0;
+        return check_launch("dequantize_many");
+    };
+    for (int t = 0; t < count; ++t) {
+        if (!(aligned(packed[t], 4) && aligned(out[t], 16)) || n[t] < 8) continue;
+        m.q[m.count] = reinterpret_cast<const uint32_t*>(packed[t]);
+        m.absmax[m.count] = absmax[t];
+        m.out[m.count] = out[t];
+        m.ngroups[m.count] = n[t] / 8;
+        if (++m.count == kManyMax) {
+            const int rc = flush();
+            if (rc) return rc;
+        }
+    }
+    int rc = flush();
+    if (rc) return rc;
+    for (int t = 0; t < count; ++t) {
+        const bool batched = aligned(packed[t], 4) && aligned(out[t], 16) && n[t] >= 8;
+        const int64_t start = batched ? n[t] / 8 * 8 : 0;
+        if (start >= n[t]) continue;
+        dim3 g((unsigned)((n[t] - start + 255) / 256)), b(256);
+        if (out_dtype == STM_F16)
+            hipLaunchKernelGGL(k_dequantize_generic<STM_F16>, g, b, 0, stream, packed[t], absmax[t], out[t], start,
+                               n[t], bshift);
+        else if (out_dtype == STM_BF16)
+            hipLaunchKernelGGL(k_dequantize_generic<STM_BF16>, g, b, 0, stream, packed[t], absmax[t], out[t], start,
+                               n[t], bshift);
+        else
+            hipLaunchKernelGGL(k_dequantize_generic<STM_F32>, g, b, 0, stream, packed[t], absmax[t], out[t], start,
+                               n[t], bshift);
+        if ((rc = check_launch("dequantize_many(tail)")) != STM_OK) return rc;
+    }
+    return STM_OK;
 }
 
 }  // namespace stm

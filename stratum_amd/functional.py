@@ -223,6 +223,102 @@ def dequantize_4bit(A: torch.Tensor, quant_state: Optional[QuantState] = None, a
     return out
 
 
+def _ptr_array(values, ctype=None):
+    import ctypes
+    ctype = ctype or ctypes.c_void_p
+    return (ctype * max(1, len(values)))(*values)
+
+
+@torch.no_grad()
+def quantize_4bit_many(tensors: Sequence[torch.Tensor], blocksize: int = 64, *,
+                       rounding: str = DEFAULT_ROUNDING) -> list:
+    """``[quantize_4bit(t, blocksize=blocksize, rounding=rounding) for t in tensors]``
+    with the whole blocks of up to 32 tensors in one launch (bit-identical
+    results). All tensors must share a dtype and a GPU."""
+    if rounding not in ROUNDING_RULES:
+        raise ValueError(f"rounding must be one of {sorted(ROUNDING_RULES)}, got {rounding!r}")
+    _check_nf4("nf4", blocksize)
+    if not tensors:
+        return []
+    dtypes = {t.dtype for t in tensors}
+    if len(dtypes) != 1:
+        raise ValueError(f"quantize_4bit_many takes one dtype per call, got {sorted(map(str, dtypes))}")
+    dtype = dtypes.pop()
+    tag = _lib.dtype_tag(dtype)
+    dev = _gpu_device(tensors[0])
+    srcs = [_aligned(t.detach().to(dev)) for t in tensors]
+    if any(x.device != dev for x in srcs):
+        raise ValueError("quantize_4bit_many takes tensors of one device")
+    ns = [x.numel() for x in srcs]
+    packed = [torch.empty(((n + 1) // 2, 1), dtype=torch.uint8, device=dev) for n in ns]
+    ams = [torch.empty(-(-n // blocksize), dtype=torch.float32, device=dev) for n in ns]
+    import ctypes
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_nf4_quantize_many(
+            len(srcs), _ptr_array([x.data_ptr() for x in srcs]), _ptr_array(ns, ctypes.c_int64), tag, blocksize,
+            ROUNDING_RULES[rounding], _ptr_array([p.data_ptr() for p in packed]),
+            _ptr_array([a.data_ptr() for a in ams]), _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_quantize_many")
+    out = []
+    for t, p, a in zip(tensors, packed, ams):
+        if not t.is_cuda:
+            p, a = p.to(t.device), a.to(t.device)
+        out.append((p, QuantState(absmax=a, shape=t.shape, code=get_4bit_type("nf4", device=a.device),
+                                  blocksize=blocksize, quant_type="nf4", dtype=t.dtype)))
+    return out
+
+
+@torch.no_grad()
+def dequantize_4bit_many(items: Sequence[tuple], *, dtype: Optional[torch.dtype] = None,
+                         out: Optional[Sequence[torch.Tensor]] = None) -> list:
+    """``[dequantize_4bit(packed, state, dtype=dtype) for packed, state in items]``
+    with the whole 8-element groups of up to 32 tensors in one launch
+    (bit-identical results). All items must share blocksize, output dtype and
+    GPU; ``out`` (optional) gives the output tensors."""
+    if not items:
+        return []
+    states = [st for _, st in items]
+    bss = {st.blocksize for st in states}
+    dts = {dtype or st.dtype for st in states}
+    if len(bss) != 1 or len(dts) != 1:
+        raise ValueError("dequantize_4bit_many takes one blocksize and one output dtype per call")
+    blocksize, odt = bss.pop(), dts.pop()
+    _check_nf4("nf4", blocksize)
+    for _, st in items:
+        if st.quant_type != "nf4":
+            raise ValueError(f"only nf4 is supported, got {st.quant_type!r}")
+    dev = items[0][0].device
+    if dev.type != "cuda" or any(q.device != dev for q, _ in items):
+        raise RuntimeError("dequantize_4bit_many runs on the GPU kernel; every packed tensor must be on one GPU")
+    ns = []
+    for q, st in items:
+        n = 1
+        for d in st.shape:
+            n *= int(d)
+        if q.numel() * 2 < n:
+            raise ValueError(f"packed tensor holds {q.numel() * 2} codes, shape {tuple(st.shape)} needs {n}")
+        if st.absmax.numel() < -(-n // blocksize):
+            raise ValueError(f"absmax holds {st.absmax.numel()} blocks, need {-(-n // blocksize)}")
+        ns.append(n)
+    qs = [_aligned(q, 4) for q, _ in items]
+    ams = [_aligned(st.absmax.to(dev, torch.float32), 4) for st in states]
+    if out is None:
+        outs = [torch.empty(tuple(st.shape), dtype=odt, device=dev) for st in states]
+    else:
+        outs = list(out)
+        if len(outs) != len(items) or any(not o.is_contiguous() or o.numel() != n or o.dtype != odt or o.device != dev
+                                          for o, n in zip(outs, ns)):
+            raise ValueError("out must hold one contiguous tensor of each item's shape and the output dtype")
+    import ctypes
+    with torch.cuda.device(dev):
+        rc = _lib.lib().stm_nf4_dequantize_many(
+            len(items), _ptr_array([q.data_ptr() for q in qs]), _ptr_array([a.data_ptr() for a in ams]),
+            _ptr_array(ns, ctypes.c_int64), blocksize, _ptr_array([o.data_ptr() for o in outs]),
+            _lib.dtype_tag(odt), _lib.stream_handle(dev))
+    _lib.check(rc, "stm_nf4_dequantize_many")
+    return outs
+
+
 # ------------------------------------------------------------ fused GEMMs
 def _gemm_dtype(t: torch.Tensor) -> int:
     if t.dtype not in (torch.bfloat16, torch.float16):

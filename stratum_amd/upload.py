@@ -47,7 +47,7 @@ from typing import Iterable, Iterator, Optional, Sequence
 
 import torch
 
-from .functional import DEFAULT_ROUNDING, QuantState, dequantize_4bit, get_4bit_type, quantize_4bit
+from .functional import DEFAULT_ROUNDING, QuantState, dequantize_4bit_many, get_4bit_type, quantize_4bit
 from .utils import log_event
 
 NF4_ATTR = "roundpipe_nf4_payload"
@@ -465,20 +465,31 @@ def _hand_over(t: torch.Tensor, consumers: list) -> torch.Tensor:
     return t
 
 
-def _dequantize_payload(payload: NF4Payload, q_dev: torch.Tensor, absmax_dev: torch.Tensor,
-                        consumers: Optional[Iterable] = None) -> torch.Tensor:
-    """The weight of *payload* from its packed bytes already on the device
-    (current stream), handed over to the consumer streams."""
-    state = QuantState(absmax=absmax_dev, shape=payload.shape, code=payload.code, blocksize=payload.blocksize,
-                       quant_type=payload.quant_type, dtype=payload.dtype)
-    w = dequantize_4bit(q_dev, state)
-    return _hand_over(w, _consumers(w.device, consumers))
-
-
 def _upload_nf4(payload: NF4Payload, device: torch.device):
     """Packed codes and absmax of *payload* on *device* (asynchronous from pinned
     memory, on the current stream)."""
     return (payload.quantized.to(device, non_blocking=True), payload.absmax.to(device, non_blocking=True))
+
+
+def _materialise_nf4(entries: list, device: torch.device, consumers: list) -> int:
+    """Bring NF4 parameters to *device* on the current stream: H2D of each packed
+    payload (or its prefetched copy), then one batched dequantize per
+    (blocksize, dtype) group -- a layer's projections in one launch.
+    *entries*: (slot, param, payload, prefetched (q, absmax) or None)."""
+    if not entries:
+        return 0
+    groups: dict = {}
+    with torch.cuda.device(device):
+        for slot, p, payload, prefetched in entries:
+            q_dev, a_dev = prefetched if prefetched is not None else _upload_nf4(payload, device)
+            state = QuantState(absmax=a_dev, shape=payload.shape, code=payload.code, blocksize=payload.blocksize,
+                               quant_type=payload.quant_type, dtype=payload.dtype)
+            groups.setdefault((payload.blocksize, payload.dtype), []).append((slot, p, q_dev, state))
+        for members in groups.values():
+            weights = dequantize_4bit_many([(q, st) for _, _, q, st in members])
+            for (slot, p, _, _), w in zip(members, weights):
+                _replace_param_data(p, _hand_over(w, consumers), owner=slot.owner, pname=slot.name)
+    return len(entries)
 
 
 def _needs(p: torch.nn.Parameter, device: torch.device) -> bool:
@@ -487,15 +498,13 @@ def _needs(p: torch.nn.Parameter, device: torch.device) -> bool:
     return p.data.numel() == 0 or p.data.device != device
 
 
-def _materialise(slot: _Slot, p: torch.nn.Parameter, device: torch.device, consumers: list,
-                 prefetched=None) -> int:
-    """Bring one parameter to *device* on the current stream; returns 1 if a
-    tensor was placed. NF4: H2D of the packed payload (or the prefetched copy)
-    and dequantize; FP16-staged: H2D copy; other frozen parameters are moved,
-    trainable ones on another device are an error (Stratum never moves them)."""
-    nf4 = getattr(p, NF4_ATTR, None)
-    fp16 = getattr(p, FP16_ATTR, None) if nf4 is None else None
-    if nf4 is None and fp16 is None:
+def _materialise(slot: _Slot, p: torch.nn.Parameter, device: torch.device, consumers: list) -> int:
+    """Bring one non-NF4 parameter to *device* on the current stream; returns 1
+    if a tensor was placed. FP16-staged: H2D copy; other frozen parameters are
+    moved, trainable ones on another device are an error (Stratum never moves
+    them). NF4 parameters go through ``_materialise_nf4``."""
+    fp16 = getattr(p, FP16_ATTR, None)
+    if fp16 is None:
         if p.data.numel() == 0 or p.data.device == device:
             return 0
         if p.requires_grad:
@@ -505,15 +514,9 @@ def _materialise(slot: _Slot, p: torch.nn.Parameter, device: torch.device, consu
         return 1
     if not _needs(p, device):
         return 0
-    if nf4 is not None:
-        q_dev, a_dev = prefetched if prefetched is not None else _upload_nf4(nf4, device)
-        with torch.cuda.device(device):
-            w = _dequantize_payload(nf4, q_dev, a_dev, consumers)
-    else:
-        w = torch.empty(fp16.shape, dtype=fp16.dtype, device=device)
-        w.copy_(fp16.data, non_blocking=True)
-        _hand_over(w, consumers)
-    _replace_param_data(p, w, owner=slot.owner, pname=slot.name)
+    w = torch.empty(fp16.shape, dtype=fp16.dtype, device=device)
+    w.copy_(fp16.data, non_blocking=True)
+    _replace_param_data(p, _hand_over(w, consumers), owner=slot.owner, pname=slot.name)
     return 1
 
 
@@ -548,7 +551,15 @@ def ensure_weights(module: torch.nn.Module, device_id: int, *, consumers: Option
     device = _cuda(device_id)
     plan = _plan(module)
     readers = _consumers(device, consumers)
-    placed = sum(_materialise(slot, p, device, readers) for slot, p in plan.unique_params())
+    placed, nf4 = 0, []
+    for slot, p in plan.unique_params():
+        payload = getattr(p, NF4_ATTR, None)
+        if payload is not None:
+            if _needs(p, device):
+                nf4.append((slot, p, payload, None))
+        else:
+            placed += _materialise(slot, p, device, readers)
+    placed += _materialise_nf4(nf4, device, readers)
     return placed + _materialise_buffers(plan, device)
 
 
@@ -624,15 +635,15 @@ class NF4Prefetch:
         if self.event is not None:
             current.wait_event(self.event)
         readers = _consumers(device, consumers)
-        placed = 0
+        todo = []
         for e in self.entries:
             if not _needs(e.param, device):
                 continue  # materialised meanwhile (e.g. by an ensure_weights)
             e.quantized.record_stream(current)  # allocated on the copy stream, read here
             e.absmax.record_stream(current)
-            placed += _materialise(e.slot, e.param, device, readers, prefetched=(e.quantized, e.absmax))
+            todo.append((e.slot, e.param, e.payload, (e.quantized, e.absmax)))
         self.entries = []
-        return placed
+        return _materialise_nf4(todo, device, readers)
 
     def wait(self) -> int:
         return self.finalize()

@@ -188,6 +188,111 @@ def test_all_zero_block_dequantizes_to_negative_zero(cuda):
     assert np.all(bits[0] == 0x8000)  # code 0 (-1.0) * 0.0 = -0.0, as the reference computes it
 
 
+# ------------------------------------------------- many tensors per launch
+MANY_SHAPES = [(5632, 2048), (256, 2048), (2048, 5632), (1001,), (3, 100), (64, 1024), (8,), (7,), (0,),
+               (129, 64)]
+
+
+@pytest.mark.parametrize("dtype,bs", [(torch.float16, 64), (torch.bfloat16, 64), (torch.float32, 128),
+                                      (torch.float16, 256), (torch.bfloat16, 4096)])
+def test_quantize_many_matches_the_oracle_per_tensor(cuda, dtype, bs):
+    """Ragged sizes (partial last blocks, odd lengths, an empty tensor) and 44
+    tensors (two launches of at most 32): every packed array and absmax
+    bit-exact against the C oracle."""
+    from stratum_amd.functional import quantize_4bit_many
+    shapes = MANY_SHAPES + [(64 * (i + 1),) for i in range(34)]
+    xs = [seeded(sh, 500 + i, 0.02 if dtype != torch.float32 else 1.0, dtype) for i, sh in enumerate(shapes)]
+    got = quantize_4bit_many([x.to(cuda) for x in xs], blocksize=bs)
+    assert len(got) == len(xs)
+    for i, (x, (p, st)) in enumerate(zip(xs, got)):
+        if x.numel() == 0:
+            assert p.numel() == 0 and st.absmax.numel() == 0
+            continue
+        rp, ra = oracle_quant(x, bs)
+        assert st.shape == x.shape and st.dtype == dtype and st.blocksize == bs
+        np.testing.assert_array_equal(p.cpu().numpy().ravel(), rp, err_msg=f"tensor {i} {tuple(x.shape)}")
+        np.testing.assert_array_equal(host_bits(st.absmax), ra.view(np.uint32), err_msg=f"tensor {i}")
+
+
+def test_quantize_many_unaligned_input_through_the_abi(cuda):
+    """A tensor 2 bytes past its allocation (no whole-block batching) beside
+    aligned ones: all bit-exact."""
+    import ctypes
+    from stratum_amd import _lib
+    base = seeded((4097,), 9, 0.02, torch.float16)
+    others = [seeded((2048,), 10, 0.02, torch.float16), seeded((1000,), 11, 0.02, torch.float16)]
+    srcs = [base.to(cuda)[1:]] + [o.to(cuda) for o in others]
+    ns = [4096, 2048, 1000]
+    ps = [torch.empty((n + 1) // 2, dtype=torch.uint8, device=cuda) for n in ns]
+    As = [torch.empty(-(-n // 64), dtype=torch.float32, device=cuda) for n in ns]
+    arr = lambda v, t=ctypes.c_void_p: (t * len(v))(*v)
+    rc = _lib.lib().stm_nf4_quantize_many(3, arr([x.data_ptr() for x in srcs]), arr(ns, ctypes.c_int64),
+                                          _lib.STM_F16, 64, _lib.STM_NF4_ARGMIN, arr([p.data_ptr() for p in ps]),
+                                          arr([a.data_ptr() for a in As]), _lib.stream_handle(cuda))
+    assert rc == 0, _lib.lib().stm_last_error()
+    for x, p, a in zip([base[1:].contiguous()] + others, ps, As):
+        rp, ra = oracle_quant(x, 64)
+        np.testing.assert_array_equal(p.cpu().numpy(), rp)
+        np.testing.assert_array_equal(host_bits(a), ra.view(np.uint32))
+
+
+@pytest.mark.parametrize("out_dtype,bs", [(torch.float16, 64), (torch.bfloat16, 64), (torch.float32, 256),
+                                          (torch.bfloat16, 4096)])
+def test_dequantize_many_matches_the_oracle_per_tensor(cuda, out_dtype, bs):
+    """The same ragged set (and 44 tensors) dequantized in batched launches,
+    into fresh outputs and into given ones, one of them misaligned: bit-exact
+    against the C oracle."""
+    from stratum_amd.functional import QuantState, dequantize_4bit_many
+    shapes = MANY_SHAPES + [(64 * (i + 1),) for i in range(34)]
+    xs = [seeded(sh, 700 + i, 0.02, torch.float16) for i, sh in enumerate(shapes)]
+    items, want = [], []
+    for x in xs:
+        rp, ra = oracle_quant(x, bs)
+        st = QuantState(absmax=torch.from_numpy(ra).to(cuda), shape=x.shape, code=None, blocksize=bs,
+                        quant_type="nf4", dtype=torch.float16)
+        items.append((torch.from_numpy(rp).reshape(-1, 1).to(cuda), st))
+        w = C.dequantize(rp, ra, x.numel(), bs, TAG[out_dtype])
+        want.append(w.view(np.uint32) if out_dtype == torch.float32 else w)
+    outs = dequantize_4bit_many(items, dtype=out_dtype)
+    for i, (o, w) in enumerate(zip(outs, want)):
+        assert o.dtype == out_dtype and o.shape == shapes[i]
+        np.testing.assert_array_equal(host_bits(o).ravel(), w, err_msg=f"tensor {i} {shapes[i]}")
+    buf = torch.empty(5632 * 2048 + 1, dtype=out_dtype, device=cuda)
+    given = [buf[1:].view(5632, 2048)] + [torch.empty(sh, dtype=out_dtype, device=cuda) for sh in shapes[1:]]
+    dequantize_4bit_many(items, dtype=out_dtype, out=given)
+    for i, (o, w) in enumerate(zip(given, want)):
+        np.testing.assert_array_equal(host_bits(o).ravel(), w, err_msg=f"given output {i}")
+
+
+def test_ensure_weights_dequantizes_a_layer_in_one_launch(cuda):
+    """A module with four NF4 projections (and a small plain parameter):
+    ensure_weights places all of them with one batched dequantize launch, each
+    weight bit-exact against the oracle."""
+    import torch.nn as nn
+    from stratum_amd.upload import ensure_weights, free_weights, prepare_nf4
+    m = nn.Module()
+    shapes = {"q": (512, 256), "k": (128, 256), "up": (1024, 256), "down": (256, 1024)}
+    for seed, (name, (n, k)) in enumerate(shapes.items()):
+        lin = nn.Linear(k, n, bias=False, dtype=torch.float16)
+        with torch.no_grad():
+            lin.weight.copy_(seeded((n, k), 900 + seed, 0.02, torch.float16))
+        setattr(m, name, lin)
+    m.norm = nn.Parameter(torch.ones(256, dtype=torch.float16))
+    m.requires_grad_(False)
+    want = {name: C.dequantize(*oracle_quant(getattr(m, name).weight.data, 64), n * k, 64, O.DT_F16)
+            for name, (n, k) in shapes.items()}
+    prepare_nf4(m, verbose=False, min_numel=4096)
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        ensure_weights(m, 0)
+        torch.cuda.synchronize()
+    names = [e.name for e in prof.events() if "k_dequantize" in e.name]
+    if names:  # the profiler saw device kernels
+        assert len(names) == 1 and "k_dequantize_many" in names[0], names
+    for name in shapes:
+        np.testing.assert_array_equal(host_bits(getattr(m, name).weight).ravel(), want[name], err_msg=name)
+    free_weights(m)
+
+
 def test_roundtrip_is_idempotent_at_8b_mlp_size(cuda):
     """quantize(dequantize(quantize(W))) == quantize(W) at the full [14336, 4096] size."""
     from stratum_amd.functional import dequantize_4bit, quantize_4bit

@@ -98,17 +98,18 @@ def test_packed_resident_layers_never_dequantize(cuda, monkeypatch):
     assert make_nf4_resident(resident, 0) == 4
     assert all(isinstance(m, NF4Linear) for blk in resident for m in (blk.up, blk.down))
     calls = []
-    real_entry = _lib.lib().stm_nf4_dequantize
+    for entry in ("stm_nf4_dequantize", "stm_nf4_dequantize_many"):
+        real_entry = getattr(_lib.lib(), entry)
 
-    def counting(*a):
-        calls.append(a)
-        return real_entry(*a)
-    monkeypatch.setattr(_lib.lib(), "stm_nf4_dequantize", counting)
+        def counting(*a, _real=real_entry, _name=entry):
+            calls.append(_name)
+            return _real(*a)
+        monkeypatch.setattr(_lib.lib(), entry, counting)
     with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
         out, dx = _run(resident, x, dy, before=lambda l: U.ensure_weights(l, 0),
                        after=lambda l: U.free_weights(l))
         torch.cuda.synchronize()
-    assert calls == [], "the resident layers called the dequantize entry point"
+    assert calls == [], f"the resident layers called {sorted(set(calls))}"
     names = [e.key for e in prof.key_averages()]
     assert not any("k_dequantize" in n for n in names), names
     if any("k_" in n for n in names):  # the profiler saw device kernels: the fused GEMMs ran
