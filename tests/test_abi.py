@@ -93,6 +93,23 @@ def test_invalid_arguments_are_rejected_without_a_gpu(L):
     assert L.stm_nf4_gemm_fwd(p + 2, p, p, None, None, None, 0, p, 4, 8, 64, 64, 1, None, 0, None) == -1
     assert L.stm_nf4_grouped_gemm_fwd(p, p, p, None, None, 4, 16, p, 8, 64, 64, 1, None) == -1
     assert L.stm_nf4_grouped_gemm_fwd(p, p, p, p, None, 0, 16, p, 8, 64, 64, 1, None) == -1
+    # batched (de)quantize: argument checks before any launch
+    i64 = (ctypes.c_int64 * 1)(-1)
+    ptrs = (ctypes.c_void_p * 1)(p)
+    assert L.stm_nf4_quantize_many(-1, None, None, 0, 64, 0, None, None, None) == -1
+    assert L.stm_nf4_quantize_many(0, None, None, 0, 64, 0, None, None, None) == 0   # nothing to do
+    assert L.stm_nf4_quantize_many(1, None, None, 0, 64, 0, None, None, None) == -1  # NULL arrays
+    assert L.stm_nf4_quantize_many(1, ptrs, i64, 0, 64, 0, ptrs, ptrs, None) == -1   # n < 0
+    assert L.stm_nf4_quantize_many(1, ptrs, i64, 0, 96, 0, ptrs, ptrs, None) == -1   # blocksize
+    assert L.stm_nf4_quantize_many(1, ptrs, i64, 0, 64, 7, ptrs, ptrs, None) == -1   # rule
+    assert L.stm_nf4_dequantize_many(-1, None, None, None, 64, None, 0, None) == -1
+    assert L.stm_nf4_dequantize_many(0, None, None, None, 64, None, 0, None) == 0
+    assert L.stm_nf4_dequantize_many(1, ptrs, ptrs, i64, 64, ptrs, 0, None) == -1    # n < 0
+    assert L.stm_nf4_dequantize_many(1, ptrs, ptrs, i64, 64, ptrs, 9, None) == -1    # dtype
+    nulls = (ctypes.c_void_p * 1)(None)
+    i64[0] = 64
+    assert L.stm_nf4_dequantize_many(1, nulls, ptrs, i64, 64, ptrs, 0, None) == -1   # NULL tensor pointer
+    assert "NULL pointer for tensor 0" in _err(L)
     assert L.stm_nf4_grouped_tile_rows(None, 4) == -1
     assert L.stm_nf4_grouped_tile_rows(p, 0) == -1
     assert L.stm_nf4_decision_boundaries(3, p) == -1
