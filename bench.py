@@ -684,8 +684,10 @@ def run_small_m(torch, args):
 
 def run_profile(args):
     """Kernel-only pass for rocprofv3 (kernel trace / PMC): each kernel of the
-    step launched `--kernel-reps` times on the default workload, plus a plain
-    1 GiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    step launched `--kernel-reps` times on the default workload, the quantize
+    kernel on the same weight, the batched quantize / dequantize on one
+    TinyLlama-1.1B layer's matrices, plus a plain 1 GiB device copy whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters."""
     import torch
 
     from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd, quantize_4bit
@@ -698,6 +700,13 @@ def run_profile(args):
     x = seeded(torch, (M, K), 1, 1.0, torch.bfloat16, dev)
     dy = seeded(torch, (M, N), 4, 1.0, torch.bfloat16, dev)
     out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    # the quantize kernel on the same weight, and the batched kernels on the
+    # matrices of one TinyLlama-1.1B layer
+    from stratum_amd.functional import dequantize_4bit_many, quantize_4bit_many
+    layer = [seeded(torch, sh, 60 + i, 0.02, torch.float16, dev) for i, sh in enumerate(
+        [(2048, 2048), (256, 2048), (256, 2048), (2048, 2048), (5632, 2048), (5632, 2048), (2048, 5632)])]
+    layer_q = quantize_4bit_many(layer)
+    layer_out = [torch.empty_like(t) for t in layer]
     # calibration: an elementwise kernel that reads 1 GiB and writes 1 GiB
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -705,6 +714,9 @@ def run_profile(args):
         nf4_gemm_fwd(x, packed, state.absmax, (N, K), 64)
         nf4_gemm_bwd_dx(dy, packed, state.absmax, (N, K), 64)
         dequantize_4bit(packed, state, out=out)
+        quantize_4bit(w)
+        quantize_4bit_many(layer)
+        dequantize_4bit_many(layer_q, out=layer_out)
         torch.mul(src, 2.0, out=dst)
     torch.cuda.synchronize()
     print(json.dumps({"profile": "done", "reps": args.kernel_reps, "copy_bytes": 4 * src.numel()}), flush=True)
