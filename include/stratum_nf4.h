@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define STM_NF4_ABI_VERSION 3
+#define STM_NF4_ABI_VERSION 4
 
 /* return codes */
 #define STM_OK 0

@@ -25,7 +25,7 @@ STM_ERR_HIP = -3
 STM_F16, STM_BF16, STM_F32 = 0, 1, 2
 STM_NF4_ARGMIN, STM_NF4_THRESHOLD = 0, 1
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # (name, argtypes) of every entry point of include/stratum_nf4.h
 _P = ctypes.c_void_p

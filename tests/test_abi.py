@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version(L):
-    assert L.stm_nf4_abi_version() == 3
+    assert L.stm_nf4_abi_version() == 4
 
 
 @pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
