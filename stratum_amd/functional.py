@@ -420,7 +420,8 @@ def _device_offsets(host_off, dev: torch.device):
     caching host allocator keeps the pinned block until the copy has run). The
     last few arrays are kept per device, so the projections of one MoE layer
     (gate/up, down, their input gradients) upload their shared offsets once; a
-    hit from another stream waits on the upload's event first.
+    hit from another stream waits on the upload's event first and hands the
+    array over to that stream.
     """
     key = (dev.index, host_off.tobytes())
     hit = _OFFSETS_CACHE.get(key)
@@ -430,6 +431,7 @@ def _device_offsets(host_off, dev: torch.device):
         staged, off, done, upload_stream = hit
         if upload_stream != stream:
             stream.wait_event(done)
+            off.record_stream(stream)  # an eviction must not free it under this stream's kernels
         return staged, off
     staged = torch.empty(host_off.shape[0], dtype=torch.int32, pin_memory=True)
     staged.numpy()[:] = host_off

@@ -449,6 +449,33 @@ def test_grouped_gemm_matches_per_expert_reference(cuda, dtype):
         assert _rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype]
 
 
+def test_grouped_gemm_host_offsets_cached_across_streams(cuda):
+    """Host (CPU) offsets are validated and uploaded once, then reused: the same
+    array on the default stream, then on a side stream that starts behind a
+    long sleep, then again after the cache has been filled past its size --
+    every result bit-identical to the first."""
+    from stratum_amd import functional as F
+    E, N, K = 4, 256, 256
+    w = seeded((E, N, K), 81, 0.02, torch.float16)
+    rp, ra = oracle_quant(w.reshape(-1, K), 64)
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    counts = [40, 0, 300, 17]
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    x = seeded((int(off[-1]), K), 82, 1.0, torch.bfloat16).to(cuda)
+    first = F.nf4_grouped_gemm(x, q, a, off, (N, K), 64)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(20_000_000)
+        again = F.nf4_grouped_gemm(x, q, a, off.clone(), (N, K), 64)
+    for i in range(F._OFFSETS_CACHE_SIZE + 2):  # evict the cached array
+        other = torch.tensor([0, i, i, i, int(off[-1])], dtype=torch.int32)
+        F.nf4_grouped_gemm(x, q, a, other, (N, K), 64)
+    torch.cuda.synchronize()
+    third = F.nf4_grouped_gemm(x, q, a, off, (N, K), 64)
+    assert torch.equal(again, first) and torch.equal(third, first)
+
+
 def test_entry_points_replay_correctly_in_a_hip_graph(cuda):
     """quantize, dequantize and a split-reduction GEMM (M = 16) captured into
     one HIP graph: every replay, with eager work and synchronisations between
