@@ -299,24 +299,26 @@ static int64_t quantize_workgroups(int64_t nfull) {
 }
 
 template <int DT, int L, int C, int U>
-static void quantize_many_launch(QuantMany& m, hipStream_t stream) {
+static int quantize_many_launch(QuantMany& m, hipStream_t stream) {
     m.first_wg[0] = 0;
     for (int t = 0; t < m.count; ++t) m.first_wg[t + 1] = m.first_wg[t] + quantize_workgroups<DT, L, C, U>(m.nblocks[t]);
+    if (m.first_wg[m.count] > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "quantize_many: batch too large");
     if (m.first_wg[m.count] > 0)
         hipLaunchKernelGGL((k_quantize_many<DT, L, C, U>), dim3((unsigned)m.first_wg[m.count]), dim3(256), 0, stream,
                            m);
+    return STM_OK;
 }
 
 template <int DT>
-static void quantize_many_dispatch(QuantMany& m, int bs, hipStream_t stream) {
+static int quantize_many_dispatch(QuantMany& m, int bs, hipStream_t stream) {
     switch (bs) {
-        case 64: quantize_many_launch<DT, 8, 1, 4>(m, stream); break;
-        case 128: quantize_many_launch<DT, 16, 1, 4>(m, stream); break;
-        case 256: quantize_many_launch<DT, 32, 1, 4>(m, stream); break;
-        case 512: quantize_many_launch<DT, 64, 1, 4>(m, stream); break;
-        case 1024: quantize_many_launch<DT, 64, 2, 2>(m, stream); break;
-        case 2048: quantize_many_launch<DT, 64, 4, 1>(m, stream); break;
-        default: quantize_many_launch<DT, 64, 8, 1>(m, stream); break;
+        case 64: return quantize_many_launch<DT, 8, 1, 4>(m, stream);
+        case 128: return quantize_many_launch<DT, 16, 1, 4>(m, stream);
+        case 256: return quantize_many_launch<DT, 32, 1, 4>(m, stream);
+        case 512: return quantize_many_launch<DT, 64, 1, 4>(m, stream);
+        case 1024: return quantize_many_launch<DT, 64, 2, 2>(m, stream);
+        case 2048: return quantize_many_launch<DT, 64, 4, 1>(m, stream);
+        default: return quantize_many_launch<DT, 64, 8, 1>(m, stream);
     }
 }
 
@@ -376,14 +378,15 @@ int launch_quantize_many(int count, const void* const* A, const int64_t* n, int 
     m.tab = tab;
     auto flush = [&]() -> int {
         if (m.count == 0) return STM_OK;
+        int rc;
         if (dtype == STM_F16)
-            quantize_many_dispatch<STM_F16>(m, bs, stream);
+            rc = quantize_many_dispatch<STM_F16>(m, bs, stream);
         else if (dtype == STM_BF16)
-            quantize_many_dispatch<STM_BF16>(m, bs, stream);
+            rc = quantize_many_dispatch<STM_BF16>(m, bs, stream);
         else
-            quantize_many_dispatch<STM_F32>(m, bs, stream);
+            rc = quantize_many_dispatch<STM_F32>(m, bs, stream);
         m.count = 0;
-        return check_launch("quantize_many");
+        return rc ? rc : check_launch("quantize_many");
     };
     for (int t = 0; t < count; ++t) {
         const int64_t nfull = (aligned(A[t], 16) && aligned(packed[t], 4)) ? n[t] / bs : 0;
@@ -550,12 +553,14 @@ int launch_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int
 }
 
 template <int DT>
-static void dequant_many_launch(DequantMany& m, hipStream_t stream) {
+static int dequant_many_launch(DequantMany& m, hipStream_t stream) {
     constexpr int U = 4;
     m.first_wg[0] = 0;
     for (int t = 0; t < m.count; ++t) m.first_wg[t + 1] = m.first_wg[t] + (m.ngroups[t] + U * 256 - 1) / (U * 256);
+    if (m.first_wg[m.count] > 0x7FFFFFFFLL) return set_error(STM_ERR_UNSUPPORTED, "dequantize_many: batch too large");
     if (m.first_wg[m.count] > 0)
         hipLaunchKernelGGL((k_dequantize_many<DT, U>), dim3((unsigned)m.first_wg[m.count]), dim3(256), 0, stream, m);
+    return STM_OK;
 }
 
 int launch_dequantize_many(int count, const uint8_t* const* packed, const float* const* absmax, const int64_t* n,
@@ -566,14 +571,15 @@ int launch_dequantize_many(int count, const uint8_t* const* packed, const float*
     m.gshift = bshift - 3;
     auto flush = [&]() -> int {
         if (m.count == 0) return STM_OK;
+        int rc;
         if (out_dtype == STM_F16)
-            dequant_many_launch<STM_F16>(m, stream);
+            rc = dequant_many_launch<STM_F16>(m, stream);
         else if (out_dtype == STM_BF16)
-            dequant_many_launch<STM_BF16>(m, stream);
+            rc = dequant_many_launch<STM_BF16>(m, stream);
         else
-            dequant_many_launch<STM_F32>(m, stream);
+            rc = dequant_many_launch<STM_F32>(m, stream);
         m.count = 0;
-        return check_launch("dequantize_many");
+        return rc ? rc : check_launch("dequantize_many");
     };
     for (int t = 0; t < count; ++t) {
         if (!(aligned(packed[t], 4) && aligned(out[t], 16)) || n[t] < 8) continue;
