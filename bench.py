@@ -431,7 +431,7 @@ def run_qwen06(torch, args):
     """Qwen3-0.6B layer projections at M = 4096 tokens: fused NF4 forward, and
     beside it dequantize + hipBLASLt per projection (the reference's
     architecture, bitsandbytes dequantize then a cuBLAS matmul)."""
-    from stratum_amd.functional import dequantize_4bit, nf4_gemm_fwd
+    from stratum_amd.functional import dequantize_4bit, nf4_gemm_fwd, stack_nf4
     dev = torch.device("cuda:0")
     M = 4096
     shapes = {"q": (2048, 1024), "k": (1024, 1024), "v": (1024, 1024), "o": (1024, 2048),
@@ -453,13 +453,39 @@ def run_qwen06(torch, args):
             st.dtype = torch.bfloat16
             torch.matmul(xs[K], dequantize_4bit(p, st, out=dense[k]).t(), out=outs[k])
 
+    # the projections that read the same input stacked into one NF4 weight
+    # each (q|k|v, gate|up: payload bytes back to back, stack_nf4), so the
+    # layer is 4 GEMMs; the outputs are column slices of the stacked results
+    groups = {"qkv": ["q", "k", "v"], "o": ["o"], "gate_up": ["gate", "up"], "down": ["down"]}
+    stacked = {g: stack_nf4([ws[k] for k in ks]) if len(ks) > 1 else ws[ks[0]] for g, ks in groups.items()}
+    sshape = {g: (sum(shapes[k][0] for k in ks), shapes[ks[0]][1]) for g, ks in groups.items()}
+    souts = {g: torch.empty((M, n), dtype=torch.bfloat16, device=dev) for g, (n, _) in sshape.items()}
+    sdense = {g: torch.empty(sh, dtype=torch.bfloat16, device=dev) for g, sh in sshape.items()}
+
+    def layer_stacked():
+        for g, (N, K) in sshape.items():
+            p, st = stacked[g]
+            nf4_gemm_fwd(xs[K], p, st.absmax, (N, K), 64, out=souts[g])
+
+    def library_stacked():
+        for g, (N, K) in sshape.items():
+            p, st = stacked[g]
+            st.dtype = torch.bfloat16
+            torch.matmul(xs[K], dequantize_4bit(p, st, out=sdense[g]).t(), out=souts[g])
+
     ms = event_time_ms(torch, layer, 20)
     lib_ms = event_time_ms(torch, library, 20)
+    sms = event_time_ms(torch, layer_stacked, 20)
+    slib_ms = event_time_ms(torch, library_stacked, 20)
     flops = sum(2.0 * M * N * K for N, K in shapes.values())
     return {"tokens": M, "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
             "gflop_per_layer": round(flops / 1e9, 2),
             "dequantize_plus_hipblaslt": {"layer_ms": round(lib_ms, 4), "tflops": round(flops / lib_ms / 1e9, 1)},
-            "fused_speedup": round(lib_ms / ms, 3)}
+            "fused_speedup": round(lib_ms / ms, 3),
+            "stacked_qkv_gate_up": {"what": "q|k|v and gate|up as one NF4 weight each: 4 GEMMs per layer",
+                                    "fused_layer_ms": round(sms, 4), "fused_tflops": round(flops / sms / 1e9, 1),
+                                    "dequantize_plus_hipblaslt_layer_ms": round(slib_ms, 4),
+                                    "fused_vs_reference_architecture": round(lib_ms / sms, 3)}}
 
 
 def run_layer_stream(torch, args):

@@ -319,6 +319,33 @@ def dequantize_4bit_many(items: Sequence[tuple], *, dtype: Optional[torch.dtype]
     return outs
 
 
+@torch.no_grad()
+def stack_nf4(items: Sequence[tuple]) -> tuple:
+    """One NF4 weight ``[sum N_i, K]`` from weights ``[N_i, K]`` that share K and
+    the blocksize: ``(packed, QuantState)`` with the packed bytes and absmax of
+    the items back to back -- exactly what quantizing the row-stacked weight
+    gives, since a block never straddles a row (K % blocksize == 0) and every
+    row's bytes start on a byte (K even). A GEMM on the result computes the
+    projections that read the same input (q/k/v, gate/up) as one launch, whose
+    output columns are the items' outputs side by side."""
+    if not items:
+        raise ValueError("stack_nf4 needs at least one weight")
+    states = [st for _, st in items]
+    K = int(states[0].shape[-1])
+    bs = states[0].blocksize
+    for st in states:
+        if len(st.shape) != 2 or int(st.shape[1]) != K or st.blocksize != bs or st.quant_type != "nf4":
+            raise ValueError("stack_nf4 takes 2-D nf4 weights with one K and one blocksize")
+    if K % bs or K % 2:
+        raise ValueError(f"K = {K} must be a multiple of the blocksize {bs} (and even)")
+    rows = [int(st.shape[0]) for st in states]
+    packed = torch.cat([q.reshape(-1)[: n * K // 2] for (q, _), n in zip(items, rows)]).reshape(-1, 1)
+    absmax = torch.cat([st.absmax.reshape(-1)[: n * K // bs] for st, n in zip(states, rows)])
+    state = QuantState(absmax=absmax, shape=(sum(rows), K), code=states[0].code, blocksize=bs, quant_type="nf4",
+                       dtype=states[0].dtype)
+    return packed, state
+
+
 # ------------------------------------------------------------ fused GEMMs
 def _gemm_dtype(t: torch.Tensor) -> int:
     if t.dtype not in (torch.bfloat16, torch.float16):

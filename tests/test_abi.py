@@ -326,3 +326,29 @@ def test_grouped_tile_rows_picks_the_fewest_padded_rows(L, counts, rows):
     off = np.zeros(len(counts) + 1, dtype=np.int32)
     off[1:] = np.cumsum(counts)
     assert L.stm_nf4_grouped_tile_rows(off.ctypes.data, len(counts)) == rows
+
+
+def test_stack_nf4_equals_quantizing_the_stacked_weight():
+    """Byte-concatenated payloads of weights sharing K are the payload of the
+    row-stacked weight (checked through the C oracle); mismatched K or
+    blocksize is refused."""
+    import torch
+    from stratum_amd.functional import QuantState, stack_nf4
+    g = torch.Generator().manual_seed(5)
+    ws = [(torch.randn(n, 320, generator=g) * 0.02).half() for n in (64, 8, 128)]
+
+    def payload(w, bs=64):
+        p, a = C.quantize(w.view(torch.int16).numpy().view(np.uint16), O.DT_F16, bs)
+        return torch.from_numpy(p).reshape(-1, 1), QuantState(absmax=torch.from_numpy(a), shape=w.shape,
+                                                              blocksize=bs, dtype=torch.float16)
+    p, st = stack_nf4([payload(w) for w in ws])
+    rp, ra = C.quantize(torch.cat(ws).view(torch.int16).numpy().view(np.uint16), O.DT_F16, 64)
+    np.testing.assert_array_equal(p.numpy().ravel(), rp)
+    np.testing.assert_array_equal(st.absmax.numpy(), ra)
+    assert tuple(st.shape) == (200, 320) and st.blocksize == 64 and st.dtype == torch.float16
+    with pytest.raises(ValueError):
+        stack_nf4([payload(ws[0]), payload((torch.randn(8, 256) * 0.02).half())])
+    with pytest.raises(ValueError):
+        stack_nf4([payload(ws[0]), payload(ws[1], bs=128)])
+    with pytest.raises(ValueError):
+        stack_nf4([])

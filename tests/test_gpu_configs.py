@@ -72,6 +72,34 @@ def test_qwen06_projection_forward_and_input_gradient(cuda, name, dtype):
     assert_gemm_close(dx, dy.float() @ wf, dtype, f"{name} input gradient")
 
 
+@pytest.mark.parametrize("group", [("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj")])
+def test_qwen06_stacked_projections_match_each_projection(cuda, group):
+    """q|k|v and gate|up stacked into one NF4 weight (stack_nf4): one fused
+    forward at M = 4096 whose column slices are each projection's output, within
+    the tolerance of the fp32 reference (and per 32 x 32 fragment)."""
+    from stratum_amd.functional import QuantState, nf4_gemm_fwd, stack_nf4
+    dtype = torch.bfloat16
+    M = 4096
+    K = QWEN06[group[0]][1]
+    items, refs = [], []
+    for name in group:
+        N = QWEN06[name][0]
+        seed = sum(map(ord, name))
+        rp, ra, wq = oracle_weight(seeded((N, K), seed, 0.02, torch.float16), dtype)
+        items.append((torch.from_numpy(rp).reshape(-1, 1).to(cuda),
+                      QuantState(absmax=torch.from_numpy(ra).to(cuda), shape=(N, K), blocksize=64, dtype=dtype)))
+        refs.append(wq.to(cuda).float())
+    p, st = stack_nf4(items)
+    x = seeded((M, K), 99, 1.0, dtype).to(cuda)
+    y = nf4_gemm_fwd(x, p, st.absmax, tuple(st.shape), 64)
+    col = 0
+    for name, wf in zip(group, refs):
+        n = wf.shape[0]
+        assert_gemm_close(y[:, col:col + n].contiguous(), x.float() @ wf.t().contiguous(), dtype, f"stacked {name}")
+        col += n
+    assert col == y.shape[1]
+
+
 # ------------------------------------------------------------ MoE expert bank
 def route_top8(tokens, experts, seed):
     """softmax(N(0, 1) logits) -> top-8 experts per token (transformers Qwen3-MoE
