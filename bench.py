@@ -242,6 +242,36 @@ def run_lora_step(args):
     step()
     default_elapsed = timed_steps(max(3, args.steps // 3))
     default_ms = default_elapsed * 1e3 / max(3, args.steps // 3)
+
+    # the reference's architecture for the same work: the frozen weight is
+    # dequantized for the forward (ensure_weights), freed after it, and
+    # dequantized again for the backward; the frozen F.linear and a PEFT LoRA
+    # (lora_B(lora_A(x)) * scaling) run in torch; autograd takes dX, dA, dB
+    import torch.nn.functional as F
+
+    class _ReferenceFrozenLinear(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, inp):
+            return F.linear(inp, dequantize_4bit(packed, state))
+
+        @staticmethod
+        def backward(ctx, gy):
+            return gy @ dequantize_4bit(packed, state)
+
+    def reference_step():
+        y = _ReferenceFrozenLinear.apply(x) + F.linear(F.linear(x, A), B) * 1.0
+        y.backward(dy)
+        x.grad = None
+        A.grad = None
+        B.grad = None
+
+    reference_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(max(3, args.steps // 3)):
+        reference_step()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3 / max(3, args.steps // 3)
     ms = elapsed * 1e3 / args.steps
     base_flops = 2 * 2.0 * M * N * K
     lora_flops = 2.0 * M * K * R + 2.0 * M * R * N           # forward rank-16 path
@@ -323,6 +353,11 @@ def run_lora_step(args):
                                         "backward re-dequantizes",
                                 "ms_per_step": round(default_ms, 4),
                                 "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},
+        "reference_architecture_step": {"what": "dequantize for the forward and again for the backward, torch "
+                                                "F.linear + PEFT-style LoRA, autograd backward",
+                                        "ms_per_step": round(ref_ms, 4),
+                                        "tflops": round(base_flops / (ref_ms * 1e-3) / 1e12, 2),
+                                        "fused_speedup": round(ref_ms / ms, 3)},
         "lora_gflop_per_step": round(lora_flops / 1e9, 2),
         "fp16": fp16,
     }
