@@ -2227,6 +2227,10 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
     return need > gemv_need ? need : gemv_need;
 }
 
+#ifndef STM_FWD_R8_AUTO
+#define STM_FWD_R8_AUTO 1
+#endif
+
 int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     // small M: the weight-streaming kernel, when its partials have a workspace
@@ -2242,9 +2246,14 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
     int rc;
+    // unsplit single-matrix 256 x 256 tiles up to 4096 rows run the 8-wave
+    // kernel (3-7 % faster at M = 2048-4096 with N = 3072-6144; 1-2 % slower at
+    // M = 8192, which keeps the 4-wave kernel); pinned kinds keep their kernel
+    const bool auto_r8 = STM_FWD_R8_AUTO && p.kind == kBig && tile_override() < 0 && g.num_groups == 1 &&
+                         g.splits == 1 && g.M <= 4096;
     if (p.kind == kBig && g.group_bm == 192 && g.num_groups > 1 && g.splits == 1 && rw && tile_override() < 0)
         rc = launch_fwd_rw<192, 1>(g, dtype, stream);
-    else if (p.kind == kBig8 && rw_offsets_fit(g))
+    else if ((p.kind == kBig8 || auto_r8) && rw_offsets_fit(g))
         rc = launch_fwd_r8(g, dtype, stream);
     else if (p.kind == kMid && rw_offsets_fit(g))
         rc = launch_fwd_rw<128, 1>(g, dtype, stream);
