@@ -2,7 +2,7 @@
 
 Bar: quantize (packed codes + absmax) and dequantize are bit-exact; fused GEMMs
 are within a relative Frobenius error of 1e-2 (bf16) / 5e-3 (fp16) of an fp32
-matmul on the oracle-dequantized weight (the tolerances the north-star states).
+matmul on the oracle-dequantized weight (the path's stated GEMM tolerances).
 """
 
 import glob
