@@ -126,6 +126,19 @@ def test_python_wrapper_raises_value_error_on_bad_arguments():
         F.quantize_4bit(torch.zeros(64, 64), compress_statistics=True)
     with pytest.raises(RuntimeError):
         F.dequantize_4bit(torch.zeros(32, 1, dtype=torch.uint8), absmax=torch.ones(1), shape=(8, 8))
+    # batched forms: argument checks before any GPU work
+    assert F.quantize_4bit_many([]) == [] and F.dequantize_4bit_many([]) == []
+    with pytest.raises(ValueError):
+        F.quantize_4bit_many([torch.zeros(64, dtype=torch.float16)], rounding="nearest")
+    with pytest.raises(ValueError):
+        F.quantize_4bit_many([torch.zeros(64, dtype=torch.float16), torch.zeros(64, dtype=torch.bfloat16)])
+    st64 = F.QuantState(absmax=torch.ones(1), shape=(8, 8), blocksize=64, dtype=torch.float16)
+    st128 = F.QuantState(absmax=torch.ones(1), shape=(8, 16), blocksize=128, dtype=torch.float16)
+    q = torch.zeros(32, 1, dtype=torch.uint8)
+    with pytest.raises(ValueError):
+        F.dequantize_4bit_many([(q, st64), (torch.zeros(64, 1, dtype=torch.uint8), st128)])
+    with pytest.raises(RuntimeError):
+        F.dequantize_4bit_many([(q, st64)])  # packed bytes on the CPU
 
 
 def test_swiglu_rejects_bad_arguments(L):
