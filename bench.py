@@ -73,7 +73,8 @@ def event_time_ms(torch, fn, reps):
     current stream (where the library launches its kernels)."""
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    fn()
+    for _ in range(3):  # warm-up: library heuristics, allocator growth
+        fn()
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(reps):
@@ -239,9 +240,13 @@ def run_lora_step(args):
             del os.environ["STRATUM_NF4_FUSED_MAX_ROWS"]
         else:
             os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = policy
-    step()
-    default_elapsed = timed_steps(max(3, args.steps // 3))
-    default_ms = default_elapsed * 1e3 / max(3, args.steps // 3)
+    # each side measurement gets warm-up steps of its own: the first steps after
+    # a switch of path run 10-15 % slow (allocator growth for the temporary
+    # weight), which one warm-up step does not absorb
+    side_warmup, side_steps = max(5, args.warmup), max(10, args.steps // 3)
+    for _ in range(side_warmup):
+        step()
+    default_ms = timed_steps(side_steps) * 1e3 / side_steps
 
     # the reference's architecture for the same work: the frozen weight is
     # dequantized for the forward (ensure_weights), freed after it, and
@@ -265,13 +270,14 @@ def run_lora_step(args):
         A.grad = None
         B.grad = None
 
-    reference_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(max(3, args.steps // 3)):
+    for _ in range(side_warmup):
         reference_step()
     torch.cuda.synchronize()
-    ref_ms = (time.perf_counter() - t0) * 1e3 / max(3, args.steps // 3)
+    t0 = time.perf_counter()
+    for _ in range(side_steps):
+        reference_step()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3 / side_steps
     ms = elapsed * 1e3 / args.steps
     base_flops = 2 * 2.0 * M * N * K
     lora_flops = 2.0 * M * K * R + 2.0 * M * R * N           # forward rank-16 path
@@ -349,7 +355,7 @@ def run_lora_step(args):
                     "traffic": traffic.get("k_dequantize")},
         "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
                         "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
-        "default_policy_step": {"what": "NF4LoRALinear default above 768 rows: dequantize + hipBLASLt, "
+        "default_policy_step": {"what": "NF4LoRALinear default above 1024 rows: dequantize + hipBLASLt, "
                                         "backward re-dequantizes",
                                 "ms_per_step": round(default_ms, 4),
                                 "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},

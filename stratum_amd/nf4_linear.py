@@ -6,9 +6,9 @@ whole weight to a temporary fp16 tensor and calls ``F.linear``
 (``stratum/nf4_linear.py:46-47``). Here each call picks the faster of two GPU
 paths for its row count M (tokens), measured on MI355X:
 
-* M <= ``fused_max_rows()`` (default 768): one fused dequant-GEMM forward and
-  one fused dequant-GEMM for ``dX = dY . W``; the dequantized weight never
-  exists in HBM, and the packed weight (0.56 B/element) is all the weight
+* M <= ``fused_max_rows()`` (default 768; 1024 with a LoRA adapter): one
+  fused dequant-GEMM forward and one fused dequant-GEMM for ``dX = dY . W``;
+  the dequantized weight never exists in HBM, and the packed weight (0.56 B/element) is all the weight
   traffic -- forward plus input gradient, the fused kernels are faster there
   (at M = 768 on the 8B-class weights: 0.22 against 0.25 ms);
 * larger M: ``dequantize_4bit`` into a temporary, then the library GEMM
@@ -41,12 +41,21 @@ from .functional import (QuantState, dequantize_4bit, fused_supported, lora_da, 
                          nf4_gemm_bwd_dx, nf4_gemm_fwd)
 
 _DEFAULT_FUSED_MAX_ROWS = 768
+# With a LoRA adapter the fused kernels fold the rank-R terms into their
+# epilogues, while the library path pays extra passes over Y and dX for them, so
+# the crossover sits higher: forward + backward on the 8B-class weights at
+# M = 1024, 0.30-0.32 ms fused against 0.33 ms; even at 1536-2048 rows;
+# library ahead from 4096 rows (8192: 1.81 against 1.70 ms).
+_DEFAULT_FUSED_MAX_ROWS_LORA = 1024
 
 
-def fused_max_rows() -> int:
-    """Largest row count (tokens) sent to the fused kernels; -1 = no limit."""
+def fused_max_rows(lora: bool = False) -> int:
+    """Largest row count (tokens) sent to the fused kernels; -1 = no limit.
+    ``STRATUM_NF4_FUSED_MAX_ROWS`` overrides both defaults."""
     v = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
-    return int(v) if v not in (None, "") else _DEFAULT_FUSED_MAX_ROWS
+    if v not in (None, ""):
+        return int(v)
+    return _DEFAULT_FUSED_MAX_ROWS_LORA if lora else _DEFAULT_FUSED_MAX_ROWS
 
 
 def _mm_scaled(a: torch.Tensor, b: torch.Tensor, scaling: float) -> torch.Tensor:
@@ -136,7 +145,7 @@ def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState
     rank = lora_a.shape[0] if lora_a is not None else 0
     if x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and rank % 16 == 0:
         rows = x.numel() // max(K, 1)
-        limit = fused_max_rows()
+        limit = fused_max_rows(lora=rank > 0)
         fused = fused_supported(N, K, bs, backward=True) and (limit < 0 or rows <= limit)
         return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling, fused)
     # unfused GPU path: dequantize into a temporary, then the library GEMM

@@ -244,8 +244,8 @@ def test_layer_stream_materialises_each_layer_then_frees_it(cuda):
 
 
 def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
-    """Default threshold: 768 rows fused, 769 rows through the library GEMM; both
-    agree with the fp32 reference."""
+    """Default threshold: 768 rows fused, 769 rows through the library GEMM (with
+    a LoRA adapter 1024 and 1025); every call agrees with the fp32 reference."""
     import importlib
     from stratum_amd.functional import quantize_4bit
     NL = importlib.import_module("stratum_amd.nf4_linear")  # the package exports a function of that name
@@ -263,6 +263,21 @@ def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
         x = seeded((M, K), 22, 1.0, torch.bfloat16).to(cuda)
         y = NL.NF4Linear(q, st)(x)
         ref = x.float() @ wq.t().contiguous()
+        assert ((y.float() - ref).norm() / ref.norm()).item() <= 1e-2
+    assert calls == [True, False]
+
+    # with a LoRA adapter the threshold is 1024 rows
+    assert NL.fused_max_rows(lora=True) == 1024
+    calls.clear()
+    lin = NL.NF4LoRALinear(q, st, r=16, lora_alpha=16.0).to(cuda)
+    with torch.no_grad():
+        lin.lora_B.copy_(seeded((N, 16), 23, 0.01, torch.float32).to(cuda))
+    a, b = lin.lora_A.detach().float(), lin.lora_B.detach().float()
+    for M in (1024, 1025):
+        x = seeded((M, K), 24, 1.0, torch.bfloat16).to(cuda)
+        y = lin(x)
+        xf = x.float()
+        ref = xf @ wq.t().contiguous() + (xf @ a.t().contiguous()) @ b.t().contiguous() * lin.scaling
         assert ((y.float() - ref).norm() / ref.norm()).item() <= 1e-2
     assert calls == [True, False]
 
