@@ -234,7 +234,8 @@ def quantize_4bit_many(tensors: Sequence[torch.Tensor], blocksize: int = 64, *,
                        rounding: str = DEFAULT_ROUNDING) -> list:
     """``[quantize_4bit(t, blocksize=blocksize, rounding=rounding) for t in tensors]``
     with the whole blocks of up to 32 tensors in one launch (bit-identical
-    results). All tensors must share a dtype and a GPU."""
+    results). All tensors must share a dtype; GPU tensors must share a device
+    (CPU tensors are copied to it, and their results back)."""
     if rounding not in ROUNDING_RULES:
         raise ValueError(f"rounding must be one of {sorted(ROUNDING_RULES)}, got {rounding!r}")
     _check_nf4("nf4", blocksize)
@@ -245,10 +246,10 @@ def quantize_4bit_many(tensors: Sequence[torch.Tensor], blocksize: int = 64, *,
         raise ValueError(f"quantize_4bit_many takes one dtype per call, got {sorted(map(str, dtypes))}")
     dtype = dtypes.pop()
     tag = _lib.dtype_tag(dtype)
-    dev = _gpu_device(tensors[0])
+    dev = _gpu_device(next((t for t in tensors if t.is_cuda), tensors[0]))
+    if any(t.is_cuda and t.device != dev for t in tensors):
+        raise ValueError("quantize_4bit_many takes the GPU tensors of one device per call")
     srcs = [_aligned(t.detach().to(dev)) for t in tensors]
-    if any(x.device != dev for x in srcs):
-        raise ValueError("quantize_4bit_many takes tensors of one device")
     ns = [x.numel() for x in srcs]
     packed = [torch.empty(((n + 1) // 2, 1), dtype=torch.uint8, device=dev) for n in ns]
     ams = [torch.empty(-(-n // blocksize), dtype=torch.float32, device=dev) for n in ns]
