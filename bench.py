@@ -372,14 +372,7 @@ def run_lora_step(args):
     if not args.main_only:
         del x, A, B, dy, out, w
         torch.cuda.empty_cache()
-        line["configs"] = {
-            "roundtrip_f16_5632x2048": run_roundtrip(torch, args),
-            "qwen3_0.6b_layer_fwd_m4096": run_qwen06(torch, args),
-            "moe_128x_gate_up_down_8192tok_top8": run_moe(torch, args),
-            "stream_8b_layers_pinned_h2d_dequant": run_layer_stream(torch, args),
-            "mlp_8b_swiglu_8192tok_chunk2048_fwd_bwd": run_mlp(torch, args),
-            "small_m16_w14336x4096_split_reduction": run_small_m(torch, args),
-        }
+        line["configs"] = {name: fn(torch, args) for name, fn in SECONDARY_CONFIGS.items()}
     return line
 
 
@@ -749,6 +742,16 @@ def run_small_m(torch, args):
             "timing": "device time: 20 launches captured in one HIP graph, replayed (split reduce included)"}
 
 
+SECONDARY_CONFIGS = {
+    "roundtrip_f16_5632x2048": run_roundtrip,
+    "qwen3_0.6b_layer_fwd_m4096": run_qwen06,
+    "moe_128x_gate_up_down_8192tok_top8": run_moe,
+    "stream_8b_layers_pinned_h2d_dequant": run_layer_stream,
+    "mlp_8b_swiglu_8192tok_chunk2048_fwd_bwd": run_mlp,
+    "small_m16_w14336x4096_split_reduction": run_small_m,
+}
+
+
 def run_profile(args):
     """Kernel-only pass for rocprofv3 (kernel trace / PMC): each kernel of the
     step launched `--kernel-reps` times on the default workload, the quantize
@@ -827,6 +830,8 @@ def main():
                     help="launch each kernel --kernel-reps times for rocprofv3; prints no bench line")
     ap.add_argument("--profile-small-m", action="store_true",
                     help="as --profile, for the M = 16 forward and input gradient")
+    ap.add_argument("--config", choices=sorted(SECONDARY_CONFIGS),
+                    help="run one secondary config alone and print its JSON (e.g. under rocprofv3)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -839,6 +844,11 @@ def main():
         return
     if args.profile_small_m:
         run_profile_small_m(args)
+        return
+    if args.config:
+        import torch
+        torch.cuda.set_device(0)
+        print(json.dumps({args.config: SECONDARY_CONFIGS[args.config](torch, args)}), flush=True)
         return
     line = run_lora_step(args)
     print(json.dumps(line), flush=True)
