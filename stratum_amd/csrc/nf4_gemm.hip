@@ -2139,14 +2139,15 @@ bool rw_split_ok(bool backward, int splits, int64_t steps) {
 }
 
 // Tile restriction: -1 = cost model, else one TileKind (tests use it to reach
-// each kernel). Starts from STRATUM_NF4_GEMM_TILE = "big", "mid" or "small",
-// read once when the library loads; stm_nf4_gemm_set_tile changes it.
+// each kernel). Starts from STRATUM_NF4_GEMM_TILE = "big", "mid", "small" or
+// "big8", read once when the library loads; stm_nf4_gemm_set_tile changes it.
 int tile_from_env() {
     const char* v = getenv("STRATUM_NF4_GEMM_TILE");
     if (!v) return -1;
     if (strcmp(v, "big") == 0) return kBig;
     if (strcmp(v, "small") == 0) return kSmall;
     if (strcmp(v, "mid") == 0) return kMid;
+    if (strcmp(v, "big8") == 0) return kBig8;
     return -1;
 }
 

@@ -365,3 +365,19 @@ def test_stack_nf4_equals_quantizing_the_stacked_weight():
         stack_nf4([payload(ws[0]), payload(ws[1], bs=128)])
     with pytest.raises(ValueError):
         stack_nf4([])
+
+
+@pytest.mark.parametrize("name,kind", [("big", 0), ("small", 1), ("mid", 2), ("big8", 3), ("bogus", -1)])
+def test_tile_env_names_map_to_tile_kinds(name, kind):
+    """STRATUM_NF4_GEMM_TILE, read once when the library loads, pins the tile
+    kind that stm_nf4_gemm_set_tile reports back (each documented name; any
+    other value leaves the cost model in charge)."""
+    import subprocess
+    import sys
+    code = ("from stratum_amd import _lib; L = _lib.lib(); "
+            "print(L.stm_nf4_gemm_set_tile(-1))")
+    env = dict(os.environ, STRATUM_NF4_GEMM_TILE=name)
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert int(out.stdout.strip().splitlines()[-1]) == kind
