@@ -29,6 +29,8 @@ work:
 
 from __future__ import annotations
 
+import weakref
+
 from typing import Any, NamedTuple, Optional
 
 import torch
@@ -122,13 +124,19 @@ class NF4StackedMLP:
             self.gu_absmax = torch.cat([ga, ua]).float()
         self.d_packed = down.quantized.reshape(-1)
         self.d_absmax = ds.absmax.reshape(-1).float()
-        self.key = self.source_key(gate, up, down)
+        # weak references, so a source freed and another tensor allocated at the
+        # same address (or with the same id) can never match
+        self.key = tuple((weakref.ref(t), t._version) for t in self._sources(gate, up, down))
 
     @staticmethod
-    def source_key(gate: NF4Linear, up: NF4Linear, down: NF4Linear) -> tuple:
-        ts = (gate.quantized, up.quantized, down.quantized, gate.quant_state.absmax, up.quant_state.absmax,
-              down.quant_state.absmax)
-        return tuple((id(t), t._version) for t in ts)
+    def _sources(gate: NF4Linear, up: NF4Linear, down: NF4Linear) -> tuple:
+        return (gate.quantized, up.quantized, down.quantized, gate.quant_state.absmax, up.quant_state.absmax,
+                down.quant_state.absmax)
+
+    def matches(self, gate: NF4Linear, up: NF4Linear, down: NF4Linear) -> bool:
+        """Built from these very tensors, none modified in place since."""
+        return all(ref() is t and version == t._version
+                   for (ref, version), t in zip(self.key, self._sources(gate, up, down)))
 
     @staticmethod
     def supported(hidden: int, inter: int, blocksize: int) -> bool:
@@ -236,7 +244,7 @@ def _nf4_stack(module: nn.Module, names: _MlpProjectionNames, x: torch.Tensor) -
     if x.shape[-1] != hidden or not NF4StackedMLP.supported(hidden, inter, gate.quant_state.blocksize):
         return None
     stack = getattr(module, _STACK_ATTR, None)
-    if stack is None or stack.key != NF4StackedMLP.source_key(gate, up, down):
+    if stack is None or not stack.matches(gate, up, down):
         stack = NF4StackedMLP(gate, up, down)
         object.__setattr__(module, _STACK_ATTR, stack)  # not a submodule, not state
     return stack

@@ -147,3 +147,33 @@ def test_silu_detection_accepts_transformers_activation():
     from stratum_amd.mlp import _is_silu
     assert _is_silu(nn.SiLU()) and _is_silu(ACT2FN["silu"])
     assert not _is_silu(nn.GELU()) and not _is_silu(torch.tanh)
+
+
+def test_stacked_nf4_weights_are_rebuilt_when_a_source_changes():
+    """The stacked [gate; up] copy is served only for the very payload tensors it
+    was built from, unmodified: an in-place update or a replacement (even one
+    that reuses the freed tensor's id or address) does not match."""
+    from stratum_amd.functional import QuantState
+    from stratum_amd.mlp import NF4StackedMLP
+    from stratum_amd.nf4_linear import NF4Linear
+
+    H, I, bs = 64, 128, 64
+
+    def lin(rows, cols, seed):
+        g = torch.Generator().manual_seed(seed)
+        q = torch.randint(0, 256, (rows * cols // 2, 1), dtype=torch.uint8, generator=g)
+        st = QuantState(absmax=torch.rand(rows * cols // bs, generator=g), shape=(rows, cols), blocksize=bs,
+                        quant_type="nf4", dtype=torch.bfloat16)
+        return NF4Linear(q, st)
+
+    gate, up, down = lin(I, H, 1), lin(I, H, 2), lin(H, I, 3)
+    stack = NF4StackedMLP(gate, up, down)
+    assert not stack.shares_storage  # separate payloads: one concatenated copy
+    assert torch.equal(stack.gu_packed, torch.cat([gate.quantized.reshape(-1), up.quantized.reshape(-1)]))
+    assert stack.matches(gate, up, down)
+    up.quant_state.absmax.mul_(1.0)  # in-place: version bump
+    assert not stack.matches(gate, up, down)
+    stack = NF4StackedMLP(gate, up, down)
+    assert stack.matches(gate, up, down)
+    gate.quantized = gate.quantized.clone()  # a new tensor with the same contents
+    assert not stack.matches(gate, up, down)
