@@ -361,6 +361,22 @@ def fused_supported(N: int, K: int, blocksize: int, backward: bool = False) -> b
     return not backward or N % 64 == 0
 
 
+def _check_weight(packed: torch.Tensor, absmax: torch.Tensor, N: int, K: int, blocksize: int, dev: torch.device,
+                  experts: int = 1) -> None:
+    """The packed codes and absmax hold ``experts`` weights of [N, K] on *dev*
+    (checked before any launch: a short tensor would be read past its end)."""
+    _check_nf4("nf4", blocksize)
+    if packed.dtype != torch.uint8 or absmax.dtype != torch.float32:
+        raise ValueError(f"packed must be uint8 and absmax float32, got {packed.dtype} and {absmax.dtype}")
+    if packed.device != dev or absmax.device != dev:
+        raise ValueError(f"packed ({packed.device}) and absmax ({absmax.device}) must be on {dev}")
+    n = experts * N * K
+    if packed.numel() * 2 < n:
+        raise ValueError(f"packed holds {packed.numel() * 2} codes, {experts} weight(s) of [{N}, {K}] need {n}")
+    if absmax.numel() * blocksize < n:
+        raise ValueError(f"absmax holds {absmax.numel()} blocks, {-(-n // blocksize)} needed")
+
+
 @torch.no_grad()
 def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, weight_shape: Sequence[int],
                  blocksize: int = 64, bias: Optional[torch.Tensor] = None, lora_t: Optional[torch.Tensor] = None,
@@ -381,6 +397,9 @@ def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, we
     x2 = _aligned(x.reshape(-1, K))
     M = x2.shape[0]
     dev = x2.device
+    _check_weight(packed, absmax, N, K, blocksize, dev)
+    if bias is not None and (bias.numel() != N or bias.device != dev):
+        raise ValueError(f"bias must hold {N} values on {dev}, got {bias.numel()} on {bias.device}")
     y = _out_buffer(out, (M, N), x.dtype, dev)
     b = _aligned(bias.to(x.dtype), 2) if bias is not None else None
     R = 0
@@ -417,6 +436,7 @@ def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
     d2 = _aligned(dy.reshape(-1, N))
     M = d2.shape[0]
     dev = d2.device
+    _check_weight(packed, absmax, N, K, blocksize, dev)
     dx = _out_buffer(out, (M, K), dy.dtype, dev)
     R = 0
     u = at = None
@@ -510,11 +530,8 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
         max_rows = largest
     elif int(max_rows) < largest:
         raise ValueError(f"max_rows = {max_rows} is below the largest expert's {largest} rows")
-    if packed.numel() * 2 < E * N * K:
-        raise ValueError(f"packed holds {packed.numel() * 2} codes, {E} experts of [{N}, {K}] need {E * N * K}")
-    if absmax.numel() * blocksize < E * N * K:
-        raise ValueError(f"absmax holds {absmax.numel()} blocks, {E * N * K // blocksize} needed")
-    if not (xin.is_cuda and packed.is_cuda and absmax.is_cuda):
+    _check_weight(packed, absmax, N, K, blocksize, dev, experts=E)
+    if not xin.is_cuda:
         raise RuntimeError("nf4_grouped_gemm runs on the GPU kernels; x, packed and absmax must be on the GPU")
     staged, off = _device_offsets(host_off, dev)
     out_cols = K if backward else N

@@ -381,3 +381,28 @@ def test_tile_env_names_map_to_tile_kinds(name, kind):
                          timeout=120)
     assert out.returncode == 0, out.stderr
     assert int(out.stdout.strip().splitlines()[-1]) == kind
+
+
+@pytest.mark.parametrize("fn", ["fwd", "bwd"])
+def test_gemm_wrappers_reject_short_or_mistyped_weights_before_launch(fn):
+    """nf4_gemm_fwd / nf4_gemm_bwd_dx check the packed codes, absmax (and bias)
+    against the weight shape on the host: a short tensor would otherwise be read
+    past its end by the kernels (CPU tensors here, so nothing is launched)."""
+    import torch
+    from stratum_amd.functional import nf4_gemm_bwd_dx, nf4_gemm_fwd
+    N, K = 128, 64
+    x = torch.zeros(4, K if fn == "fwd" else N, dtype=torch.bfloat16)
+    call = (lambda p, a, **kw: nf4_gemm_fwd(x, p, a, (N, K), 64, **kw)) if fn == "fwd" else \
+        (lambda p, a, **kw: nf4_gemm_bwd_dx(x, p, a, (N, K), 64, **kw))
+    good_p, good_a = torch.zeros(N * K // 2, dtype=torch.uint8), torch.ones(N * K // 64)
+    with pytest.raises(ValueError, match="packed holds"):
+        call(good_p[:-1], good_a)
+    with pytest.raises(ValueError, match="absmax holds"):
+        call(good_p, good_a[:-1])
+    with pytest.raises(ValueError, match="uint8"):
+        call(good_p.to(torch.int16), good_a)
+    with pytest.raises(ValueError, match="float32"):
+        call(good_p, good_a.double())
+    if fn == "fwd":
+        with pytest.raises(ValueError, match="bias"):
+            call(good_p, good_a, bias=torch.zeros(N - 1, dtype=torch.bfloat16))
