@@ -214,8 +214,9 @@ def dequantize_4bit(A: torch.Tensor, quant_state: Optional[QuantState] = None, a
     am = _aligned(absmax.to(dev, torch.float32), 4)
     if out is None:
         out = torch.empty(tuple(shape), dtype=dtype, device=dev)
-    elif not out.is_contiguous() or out.numel() != n or out.dtype != dtype:
-        raise ValueError("out must be a contiguous tensor of the quant_state shape and dtype")
+    elif not out.is_contiguous() or out.numel() != n or out.dtype != dtype or out.device != dev:
+        raise ValueError("out must be a contiguous tensor of the quant_state shape and dtype, on the packed "
+                         "tensor's device")
     with torch.cuda.device(dev):
         rc = _lib.lib().stm_nf4_dequantize(q.data_ptr(), am.data_ptr(), n, blocksize, out.data_ptr(),
                                            _lib.dtype_tag(dtype), _lib.stream_handle(dev))
@@ -361,6 +362,14 @@ def fused_supported(N: int, K: int, blocksize: int, backward: bool = False) -> b
     return not backward or N % 64 == 0
 
 
+def _on_device(dev: torch.device, **tensors) -> None:
+    """Every given tensor lives on *dev* (a pointer from another device or the
+    host would be dereferenced by the kernel)."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, the kernel runs on {dev}")
+
+
 def _check_weight(packed: torch.Tensor, absmax: torch.Tensor, N: int, K: int, blocksize: int, dev: torch.device,
                   experts: int = 1) -> None:
     """The packed codes and absmax hold ``experts`` weights of [N, K] on *dev*
@@ -398,6 +407,7 @@ def nf4_gemm_fwd(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, we
     M = x2.shape[0]
     dev = x2.device
     _check_weight(packed, absmax, N, K, blocksize, dev)
+    _on_device(dev, lora_t=lora_t, lora_b=lora_b)
     if bias is not None and (bias.numel() != N or bias.device != dev):
         raise ValueError(f"bias must hold {N} values on {dev}, got {bias.numel()} on {bias.device}")
     y = _out_buffer(out, (M, N), x.dtype, dev)
@@ -437,6 +447,7 @@ def nf4_gemm_bwd_dx(dy: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
     M = d2.shape[0]
     dev = d2.device
     _check_weight(packed, absmax, N, K, blocksize, dev)
+    _on_device(dev, lora_u=lora_u, lora_at=lora_at)
     dx = _out_buffer(out, (M, K), dy.dtype, dev)
     R = 0
     u = at = None
@@ -591,6 +602,7 @@ def swiglu_bwd(grad_out: torch.Tensor, gate_up: torch.Tensor, out: Optional[torc
     if dh.shape[0] != rows:
         raise ValueError("grad_out and gate_up have different row counts")
     dev = gu.device
+    _on_device(dev, grad_out=dh)
     dgu = _out_buffer(out, (rows, two_i), gate_up.dtype, dev) if out is not None else \
         torch.empty((rows, two_i), dtype=gate_up.dtype, device=dev)
     with torch.cuda.device(dev):
@@ -637,8 +649,9 @@ def lora_down(x: torch.Tensor, lora_a: torch.Tensor, scaling: float = 1.0) -> to
     for d in x.shape[:-1]:
         M *= int(d)
     x2 = _aligned(x.reshape(M, K))
-    a = _aligned(lora_a.to(x.dtype))
     dev = x2.device
+    _on_device(dev, lora_a=lora_a)
+    a = _aligned(lora_a.to(x.dtype))
     t = torch.empty((M, R), dtype=x.dtype, device=dev)
     with torch.cuda.device(dev):
         ws = _lora_workspace(M, K, R, 0, dev)
@@ -659,9 +672,10 @@ def lora_dy(dy: torch.Tensor, lora_b: torch.Tensor, t: Optional[torch.Tensor] = 
     if tuple(lora_b.shape) != (N, R):
         raise ValueError(f"lora_b shape {tuple(lora_b.shape)} != ({N}, {R})")
     d2 = _aligned(dy.reshape(-1, N))
-    b = _aligned(lora_b.to(dy.dtype))
     M = d2.shape[0]
     dev = d2.device
+    _on_device(dev, lora_b=lora_b, t=t)
+    b = _aligned(lora_b.to(dy.dtype))
     t2 = None
     if t is not None:
         t2 = _aligned(t.reshape(M, R).to(dy.dtype))
@@ -683,8 +697,9 @@ def lora_da(u: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     M = x2.shape[0]
     R = int(u.shape[-1])
     tag = _gemm_dtype(x)
-    u2 = _aligned(u.reshape(M, R).to(x.dtype))
     dev = x2.device
+    _on_device(dev, u=u)
+    u2 = _aligned(u.reshape(M, R).to(x.dtype))
     da = torch.empty((R, K), dtype=x.dtype, device=dev)
     with torch.cuda.device(dev):
         ws = _lora_workspace(M, K, R, 2, dev)

@@ -406,3 +406,14 @@ def test_gemm_wrappers_reject_short_or_mistyped_weights_before_launch(fn):
     if fn == "fwd":
         with pytest.raises(ValueError, match="bias"):
             call(good_p, good_a, bias=torch.zeros(N - 1, dtype=torch.bfloat16))
+
+
+def test_wrappers_refuse_operands_on_another_device():
+    """A host pointer handed to a kernel beside device ones is refused on the host
+    (here every operand but one is on the meta device, so nothing can launch)."""
+    import torch
+    from stratum_amd.functional import _on_device
+    dev = torch.device("meta")
+    _on_device(dev, a=torch.empty(2, device=dev), b=None)
+    with pytest.raises(ValueError, match="b is on cpu"):
+        _on_device(dev, a=torch.empty(2, device=dev), b=torch.zeros(2))
