@@ -152,9 +152,12 @@ def test_kernels_reproduce_golden_fixtures(cuda, path):
 
 # ------------------------------------------------------------ dequantize
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape,bs", [((5632, 2048), 64), ((14336, 4096), 64), ((128, 4096), 4096),
-                                      ((1001,), 64), ((7, 9), 64)])
+@pytest.mark.parametrize("shape,bs", [((5632, 2048), 64), ((4096, 6144), 64), ((14336, 4096), 64),
+                                      ((128, 4096), 4096), ((1001,), 64), ((7, 9), 64)])
 def test_dequantize_bit_exact(cuda, out_dtype, shape, bs):
+    """Bit-exact against the oracle; the sizes take each per-thread work size of
+    the kernel (2, 4 and 8 groups of 8 elements: under 2^24, 2^24..2^25, over)
+    and the one-element-per-thread tail."""
     from stratum_amd.functional import dequantize_4bit
     x = seeded(shape, 7, 0.02, torch.float16)
     rp, ra = oracle_quant(x, bs)
