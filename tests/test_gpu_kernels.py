@@ -54,6 +54,7 @@ def oracle_deq_tensor(packed, absmax, shape, bs, dtype):
 @pytest.mark.parametrize("rule", ["argmin", "threshold"])
 @pytest.mark.parametrize("dtype,shape,bs", [
     (torch.float16, (5632, 2048), 64),      # TinyLlama gate_proj, the CPU-runnable reference case
+    (torch.float16, (8192, 4096), 64),      # 2^19 blocks: the launch's larger per-wave work size
     (torch.bfloat16, (1024, 1024), 64),
     (torch.float32, (256, 1024), 64),
     (torch.float16, (64, 1024), 128),
