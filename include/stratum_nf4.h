@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define STM_NF4_ABI_VERSION 4
+#define STM_NF4_ABI_VERSION 5
 
 /* return codes */
 #define STM_OK 0
@@ -180,9 +180,12 @@ int stm_nf4_gemm_set_tile(int kind);
  * rows are grouped by expert. Replaces the per-expert F.linear loop of
  * transformers' Qwen3MoeExperts.forward on the dequantized stacked weight.
  *   offsets: device int32 [E + 1], offsets[0] = 0, non-decreasing, offsets[E] = M_total
- *   host_offsets: NULL, or a host copy of offsets; read before the launch to
- *             pick the tile height (stm_nf4_grouped_tile_rows). A plan hint
- *             only: the kernels index rows by the device array alone.
+ *   host_offsets: NULL, or a host copy of offsets; read before the launch:
+ *             validated (offsets[0] = 0, non-decreasing, no expert above
+ *             max_rows: else STM_ERR_INVALID, nothing launched) and used to
+ *             pick the tile height (stm_nf4_grouped_tile_rows). The kernels
+ *             index rows by the device array alone, which is NOT read on the
+ *             host: without host_offsets the caller guarantees its contract.
  *   max_rows: an upper bound on offsets[e+1] - offsets[e] (sizes the launch grid)
  *   constraints: as stm_nf4_gemm_fwd
  */
@@ -195,16 +198,20 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
  * (host int32 [E + 1] offsets): the height that computes the fewest padded
  * rows, a 192-row tile's row weighted 8 % dearer. Pure host function; no
  * counterpart in the reference (its per-expert loop has no tiles).
- * Returns 192, 256, or STM_ERR_INVALID.
+ * Returns 192, 256, or STM_ERR_INVALID (NULL, num_experts <= 0, offsets[0] != 0
+ * or decreasing offsets).
  */
 int stm_nf4_grouped_tile_rows(const int32_t* host_offsets, int num_experts);
 
 /*
  * Grouped input gradient: for each expert e: dX[rows of e] = dY[rows of e] . W_e.
+ * Replaces the autograd backward of the same per-expert F.linear loop.
+ *   host_offsets: NULL, or a host copy of offsets, validated as in the forward
+ *                 (version 5 added it).
  */
 int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const int32_t* offsets,
-                                int num_experts, int64_t max_rows, void* dX, int64_t N, int64_t K, int blocksize,
-                                int dtype, void* stream);
+                                const int32_t* host_offsets, int num_experts, int64_t max_rows, void* dX, int64_t N,
+                                int64_t K, int blocksize, int dtype, void* stream);
 
 /*
  * SwiGLU gating of a frozen MLP, between the stacked [gate; up] projection and

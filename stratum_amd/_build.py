@@ -33,21 +33,41 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *srcs]
+def _run(cmd: list, verbose: bool) -> subprocess.Popen:
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode})")
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _finish(proc: subprocess.Popen, what: str, verbose: bool) -> None:
+    out, _ = proc.communicate()
+    if proc.returncode != 0:
+        sys.stderr.write(out)
+        raise RuntimeError(f"hipcc failed building {what} (exit {proc.returncode})")
     # drop the host-compiler note about the device-only feature flag
     noise = "is not a recognized feature for this target"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if ln.strip() and noise not in ln]
+    msgs = [ln for ln in out.splitlines() if ln.strip() and noise not in ln]
     if msgs and verbose:
         print("\n".join(msgs), flush=True)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source to an object (in parallel), then link the library.
+    Objects go to a private temporary directory; nothing but the library is
+    left in the package."""
+    import tempfile
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="stm_build_") as tmpdir:
+        objs, procs = [], []
+        for src in SOURCES:
+            obj = os.path.join(tmpdir, os.path.splitext(src)[0] + ".o")
+            objs.append(obj)
+            procs.append((_run([HIPCC, *compile_flags, "-c", os.path.join(CSRC, src), "-o", obj], verbose), src))
+        for proc, src in procs:
+            _finish(proc, src, verbose)
+        tmp = LIB_PATH + ".tmp"
+        _finish(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], verbose), LIB_NAME,
+                verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

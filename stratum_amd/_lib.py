@@ -25,7 +25,7 @@ STM_ERR_HIP = -3
 STM_F16, STM_BF16, STM_F32 = 0, 1, 2
 STM_NF4_ARGMIN, STM_NF4_THRESHOLD = 0, 1
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # (name, argtypes) of every entry point of include/stratum_nf4.h
 _P = ctypes.c_void_p
@@ -45,7 +45,7 @@ SIGNATURES = {
     "stm_nf4_grouped_tile_rows": ([_P, _I], _I),
     "stm_nf4_quantize_many": ([_I, _P, _P, _I, _I, _I, _P, _P, _P], _I),
     "stm_nf4_dequantize_many": ([_I, _P, _P, _P, _I, _P, _I, _P], _I),
-    "stm_nf4_grouped_gemm_bwd_dx": ([_P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
+    "stm_nf4_grouped_gemm_bwd_dx": ([_P, _P, _P, _P, _P, _I, _I64, _P, _I64, _I64, _I, _I, _P], _I),
     "stm_swiglu_fwd": ([_P, _P, _I64, _I64, _I, _P], _I),
     "stm_swiglu_bwd": ([_P, _P, _P, _I64, _I64, _I, _P], _I),
     "stm_lora_workspace_bytes": ([_I64, _I64, _I, _I], _I64),

@@ -351,10 +351,28 @@ int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absm
     return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
 }
 
+// Host copy of a grouped call's expert offsets: offsets[0] = 0, non-decreasing,
+// and (max_rows >= 0) no expert above max_rows rows. Read entirely on the host,
+// before any launch.
+static int check_host_offsets(const char* fn, const int32_t* h, int num_experts, int64_t max_rows) {
+    if (h[0] != 0) return set_error(STM_ERR_INVALID, "%s: offsets[0] = %d, expected 0", fn, h[0]);
+    for (int e = 0; e < num_experts; ++e) {
+        const int64_t rows = (int64_t)h[e + 1] - h[e];
+        if (rows < 0)
+            return set_error(STM_ERR_INVALID, "%s: offsets decrease at expert %d (%d -> %d)", fn, e, h[e], h[e + 1]);
+        if (max_rows >= 0 && rows > max_rows)
+            return set_error(STM_ERR_INVALID, "%s: expert %d has %lld rows, above max_rows %lld", fn, e,
+                             (long long)rows, (long long)max_rows);
+    }
+    return STM_OK;
+}
+
 int stm_nf4_grouped_tile_rows(const int32_t* host_offsets, int num_experts) {
     g_err[0] = 0;
     if (!host_offsets || num_experts <= 0)
         return set_error(STM_ERR_INVALID, "grouped_tile_rows: NULL offsets or num_experts %d", num_experts);
+    const int rc = check_host_offsets("grouped_tile_rows", host_offsets, num_experts, -1);
+    if (rc != STM_OK) return rc;
     return grouped_tile_rows(host_offsets, num_experts);
 }
 
@@ -369,6 +387,8 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
     if (rc <= 0) return rc;
     if (!offsets) return set_error(STM_ERR_INVALID, "grouped_gemm_fwd: NULL offsets");
     if (N % 8 != 0) return set_error(STM_ERR_UNSUPPORTED, "grouped_gemm_fwd: N must be a multiple of 8");
+    if (host_offsets && (rc = check_host_offsets("grouped_gemm_fwd", host_offsets, num_experts, max_rows)) != STM_OK)
+        return rc;
     GemmArgs g{};
     g.a = X; g.packed = packed; g.absmax = absmax; g.out = Y; g.M = max_rows; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
@@ -377,8 +397,8 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
 }
 
 int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absmax, const int32_t* offsets,
-                                int num_experts, int64_t max_rows, void* dX, int64_t N, int64_t K, int blocksize,
-                                int dtype, void* stream) {
+                                const int32_t* host_offsets, int num_experts, int64_t max_rows, void* dX, int64_t N,
+                                int64_t K, int blocksize, int dtype, void* stream) {
     g_err[0] = 0;
     if (num_experts <= 0 || max_rows < 0)
         return set_error(STM_ERR_INVALID, "grouped_gemm_bwd_dx: num_experts %d, max_rows %lld", num_experts,
@@ -387,6 +407,9 @@ int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const flo
     if (rc <= 0) return rc;
     if (!offsets) return set_error(STM_ERR_INVALID, "grouped_gemm_bwd_dx: NULL offsets");
     if (N % 64 != 0) return set_error(STM_ERR_UNSUPPORTED, "grouped_gemm_bwd_dx: N must be a multiple of 64");
+    if (host_offsets &&
+        (rc = check_host_offsets("grouped_gemm_bwd_dx", host_offsets, num_experts, max_rows)) != STM_OK)
+        return rc;
     GemmArgs g{};
     g.a = dY; g.packed = packed; g.absmax = absmax; g.out = dX; g.M = max_rows; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;

@@ -37,12 +37,28 @@ __device__ __forceinline__ float nanmax(float a, float b) { return __builtin_ele
 // cell's entry, with no convert or shift. A NaN s (all-zero or NaN block)
 // gives f = NaN whose bits & 0x3FC are 0, and c = -1 gives f = 2^21, also
 // cell 0, whose base is code 0 and whose bound (2.0) is never met -- code 0,
-// as both bitsandbytes rules give, whether v_med3 returns the NaN or -1.
+// as both bitsandbytes rules give. v_med3_f32 with a NaN operand returns the
+// minimum of its operands (IEEE mode: the smaller non-NaN one), so a NaN s of
+// any payload becomes c = -1; should a NaN c still reach the formula, its
+// payload bits can name any cell up to 255, and the LDS tables are padded to
+// 256 cells with copies of cell 0 (see fill_cells), so the read stays inside
+// the tables and the code is still 0 for the cells above 64.
 __device__ __forceinline__ uint32_t level_of(float s, const float* __restrict__ bound,
                                              const uint32_t* __restrict__ base) {
     const float c = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
     const uint32_t j = (__float_as_uint(__builtin_fmaf(c, 32.0f, 2097184.0f)) & 0x3FCu) >> 2;
     return base[j] + (c >= bound[j] ? 1u : 0u);
+}
+
+// LDS copies of the cell table: cells 0..64 from the host table, 65..255 as
+// cell 0 (bound 2.0 is never met, base code 0), one cell per thread.
+constexpr int kLdsCells = 256;
+__device__ __forceinline__ void fill_cells(const CellTable& tab, float* s_bound, uint32_t* s_base, int tid,
+                                           int nthreads) {
+    for (int t = tid; t < kLdsCells; t += nthreads) {
+        s_bound[t] = t < 65 ? tab.bound[t] : 2.0f;
+        s_base[t] = t < 65 ? tab.base[t] : 0u;
+    }
 }
 
 template <int DT>
@@ -174,10 +190,7 @@ __device__ __forceinline__ void quantize_workgroup(const void* __restrict__ x, u
                 ch[u][c].zero();
         }
     }
-    if (threadIdx.x < 65) {
-        s_bound[threadIdx.x] = tab.bound[threadIdx.x];
-        s_base[threadIdx.x] = tab.base[threadIdx.x];
-    }
+    fill_cells(tab, s_bound, s_base, threadIdx.x, 256);
     __syncthreads();
 
     float a[U];
@@ -223,8 +236,8 @@ __device__ __forceinline__ void quantize_workgroup(const void* __restrict__ x, u
 template <int DT, int L, int C, int U>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, uint32_t* __restrict__ packed,
                                                   float* __restrict__ absmax, int64_t nblocks, CellTable tab) {
-    __shared__ float s_bound[65];
-    __shared__ uint32_t s_base[65];
+    __shared__ float s_bound[kLdsCells];
+    __shared__ uint32_t s_base[kLdsCells];
     quantize_workgroup<DT, L, C, U>(x, packed, absmax, nblocks, blockIdx.x, tab, s_bound, s_base);
 }
 
@@ -249,8 +262,8 @@ __device__ __forceinline__ int tensor_of(const int64_t* first_wg, int count, int
 
 template <int DT, int L, int C, int U>
 __global__ __launch_bounds__(256) void k_quantize_many(QuantMany m) {
-    __shared__ float s_bound[65];
-    __shared__ uint32_t s_base[65];
+    __shared__ float s_bound[kLdsCells];
+    __shared__ uint32_t s_base[kLdsCells];
     const int t = tensor_of(m.first_wg, m.count, blockIdx.x);
     quantize_workgroup<DT, L, C, U>(m.x[t], m.packed[t], m.absmax[t], m.nblocks[t], blockIdx.x - m.first_wg[t], m.tab,
                                     s_bound, s_base);
@@ -261,12 +274,9 @@ template <int DT>
 __global__ __launch_bounds__(64) void k_quantize_generic(const void* __restrict__ x, int64_t n, int bs,
                                                          int64_t b_begin, int64_t b_end, uint8_t* __restrict__ packed,
                                                          float* __restrict__ absmax, CellTable tab) {
-    __shared__ float s_bound[65];
-    __shared__ uint32_t s_base[65];
-    for (int t = threadIdx.x; t < 65; t += 64) {
-        s_bound[t] = tab.bound[t];
-        s_base[t] = tab.base[t];
-    }
+    __shared__ float s_bound[kLdsCells];
+    __shared__ uint32_t s_base[kLdsCells];
+    fill_cells(tab, s_bound, s_base, threadIdx.x, 64);
     __syncthreads();
     const int64_t blk = b_begin + (int64_t)blockIdx.x * 64 + threadIdx.x;
     if (blk >= b_end) return;

@@ -556,9 +556,9 @@ def nf4_grouped_gemm(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor
             raise ValueError(f"out must be a contiguous [{M_total}, {out_cols}] {x.dtype} tensor on {dev}")
         y = out
     fn = _lib.lib().stm_nf4_grouped_gemm_bwd_dx if backward else _lib.lib().stm_nf4_grouped_gemm_fwd
-    lead = (xin.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(), off.data_ptr())
-    if not backward:  # the host counts pick the forward's tile height
-        lead = lead + (staged.data_ptr(),)
+    # the host copy of the offsets: validated by the library, and the forward's tile height
+    lead = (xin.data_ptr(), _aligned(packed).data_ptr(), _aligned(absmax, 4).data_ptr(), off.data_ptr(),
+            staged.data_ptr())
     with torch.cuda.device(dev):
         rc = fn(*lead, E, int(max_rows), y.data_ptr(), N, K, blocksize, tag, _lib.stream_handle(dev))
     _lib.check(rc, "stm_nf4_grouped_gemm_" + ("bwd_dx" if backward else "fwd"))

@@ -14,9 +14,13 @@ paths for its row count M (tokens), measured on MI355X:
 * larger M: ``dequantize_4bit`` into a temporary, then the library GEMM
   (hipBLASLt), whose forward is 1.2-1.3x faster than the fused kernel at
   M = 2048..8192, because the dequantization is paid once for all rows instead
-  of once per 256-row tile. The backward dequantizes again instead of keeping the
-  temporary alive (23 us for a 14336 x 4096 weight), as the reference's
-  forward/recompute does.
+  of once per 256-row tile. When the call records a graph for the input
+  gradient (a recompute pass, or a plain training forward), the temporary is
+  kept for the backward, as the reference keeps ``param.data`` from its
+  recompute to its backward: the pipeline's forward, recompute and backward
+  then dequantize twice per step, as the reference does
+  (``stratum/pipeline.py:906``). ``NF4Linear.keep_weight_for_backward = False``
+  trades that for memory (the backward dequantizes again).
 
 ``NF4LoRALinear`` adds the PEFT-style LoRA update (``scripts/train.py:568-573``:
 r=16, alpha=16), folded into the fused kernels' epilogues on the first path.
@@ -29,7 +33,8 @@ never).
 from __future__ import annotations
 
 import math
-from typing import Optional
+from contextlib import contextmanager
+from typing import Optional, Sequence
 
 import torch
 import torch.nn as nn
@@ -70,7 +75,8 @@ class _NF4LinearFn(torch.autograd.Function):
     """y = x . W^T (+ bias) (+ scaling * (x . A^T) . B^T) with W frozen in NF4."""
 
     @staticmethod
-    def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused):
+    def forward(ctx, x, packed, absmax, shape, blocksize, bias, lora_a, lora_b, scaling, fused, w_dense=None,
+                keep_w=True):
         t = None
         if lora_a is not None:
             if lora_supported(lora_a.shape[0], x.shape[-1], x.numel() // max(x.shape[-1], 1)):
@@ -81,7 +87,10 @@ class _NF4LinearFn(torch.autograd.Function):
             y = nf4_gemm_fwd(x, packed, absmax, shape, blocksize, bias=bias, lora_t=t,
                              lora_b=lora_b.to(x.dtype) if lora_b is not None else None)
         else:
-            w = dequantize_4bit(packed, absmax=absmax, blocksize=blocksize, dtype=x.dtype, shape=shape)
+            if w_dense is not None and w_dense.dtype == x.dtype:
+                w = w_dense
+            else:
+                w = dequantize_4bit(packed, absmax=absmax, blocksize=blocksize, dtype=x.dtype, shape=shape)
             b = bias.to(x.dtype) if bias is not None else None
             if t is not None:
                 # rank-R term (and bias) first, then the base GEMM accumulates into it
@@ -91,6 +100,8 @@ class _NF4LinearFn(torch.autograd.Function):
                 y = y2.addmm_(x.reshape(-1, x.shape[-1]), w.t()).reshape(*x.shape[:-1], w.shape[0])
             else:
                 y = F.linear(x, w, b)
+            # needs_input_grad is all False when no graph is recorded (no_grad forward)
+            ctx.w = w if keep_w and ctx.needs_input_grad[0] else None
             del w
         ctx.shape, ctx.blocksize, ctx.scaling, ctx.fused = shape, blocksize, scaling, fused
         ctx.has_bias_grad = bias is not None and bias.requires_grad
@@ -117,7 +128,9 @@ class _NF4LinearFn(torch.autograd.Function):
                 dx = nf4_gemm_bwd_dx(dy2, packed, absmax, ctx.shape, ctx.blocksize, lora_u=u,
                                      lora_at=lora_a.t().contiguous().to(dy2.dtype) if lora_a is not None else None)
             else:
-                w = dequantize_4bit(packed, absmax=absmax, blocksize=ctx.blocksize, dtype=dy2.dtype, shape=ctx.shape)
+                w = ctx.w if ctx.w is not None and ctx.w.dtype == dy2.dtype else \
+                    dequantize_4bit(packed, absmax=absmax, blocksize=ctx.blocksize, dtype=dy2.dtype, shape=ctx.shape)
+                ctx.w = None
                 if u is not None:
                     dx = (u @ lora_a.to(dy2.dtype)).addmm_(dy2, w)     # rank-R term, then the base GEMM into it
                 else:
@@ -133,12 +146,19 @@ class _NF4LinearFn(torch.autograd.Function):
                 d_a = d_a.to(lora_a.dtype)
             if d_b is not None:
                 d_b = d_b.to(lora_b.dtype)
-        return dx, None, None, None, None, d_bias, d_a, d_b, None, None
+        ctx.w = None
+        return dx, None, None, None, None, d_bias, d_a, d_b, None, None, None, None
 
 
 def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None,
                lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
-               scaling: float = 1.0) -> torch.Tensor:
+               scaling: float = 1.0, *, w_dense: Optional[torch.Tensor] = None,
+               keep_weight_for_backward: bool = True) -> torch.Tensor:
+    """``x . W^T (+ bias) (+ scaling * (x . A^T) . B^T)`` with W in NF4.
+
+    ``w_dense``: an already dequantized W (same dtype as x) that the library
+    path uses instead of dequantizing (``NF4Linear.dense_weight``); the fused
+    path ignores it. ``keep_weight_for_backward``: see the module docstring."""
     shape = tuple(int(s) for s in quant_state.shape)
     N, K = shape
     bs = quant_state.blocksize
@@ -147,9 +167,11 @@ def nf4_linear(x: torch.Tensor, quantized: torch.Tensor, quant_state: QuantState
         rows = x.numel() // max(K, 1)
         limit = fused_max_rows(lora=rank > 0)
         fused = fused_supported(N, K, bs, backward=True) and (limit < 0 or rows <= limit)
-        return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling, fused)
+        return _NF4LinearFn.apply(x, quantized, quant_state.absmax, shape, bs, bias, lora_a, lora_b, scaling, fused,
+                                  w_dense, keep_weight_for_backward)
     # unfused GPU path: dequantize into a temporary, then the library GEMM
-    w = dequantize_4bit(quantized, quant_state, dtype=x.dtype)
+    w = w_dense if w_dense is not None and w_dense.dtype == x.dtype else dequantize_4bit(quantized, quant_state,
+                                                                                         dtype=x.dtype)
     y = F.linear(x, w, bias.to(x.dtype) if bias is not None else None)
     if lora_a is not None:
         y = y + F.linear(F.linear(x, lora_a.to(x.dtype)), lora_b.to(x.dtype)) * scaling
@@ -161,7 +183,16 @@ class NF4Linear(nn.Module):
 
     Same constructor as the reference (``stratum/nf4_linear.py:27-41``): the
     packed codes, their ``QuantState`` and an optional bias (stored frozen).
+
+    ``weight`` (read-only) dequantizes the packed weight into a new dense
+    tensor on every read, for code that reads ``module.weight`` directly (the
+    reference's chunked loss reads ``lm_head.weight``,
+    ``stratum/model/chunked_loss.py:184``); it costs a dequantization and 2
+    bytes per weight while the tensor lives. ``dense_weight()`` holds one such
+    tensor for a stretch of calls that all use it.
     """
+
+    keep_weight_for_backward = True
 
     def __init__(self, quantized: torch.Tensor, quant_state: QuantState, bias: Optional[torch.Tensor] = None):
         super().__init__()
@@ -173,9 +204,33 @@ class NF4Linear(nn.Module):
             self.bias = None
         self.in_features = quant_state.shape[1]
         self.out_features = quant_state.shape[0]
+        self._w_dense = None
+
+    @property
+    def weight(self) -> torch.Tensor:
+        """The dequantized weight ``[out_features, in_features]`` in the
+        payload's source dtype: a new tensor per read (see the class docstring)."""
+        if self._w_dense is not None:
+            return self._w_dense
+        return dequantize_4bit(self.quantized, self.quant_state)
+
+    @contextmanager
+    def dense_weight(self, dtype: Optional[torch.dtype] = None):
+        """Dequantize once and let every call inside the block that takes the
+        library path (and ``weight``) use that tensor; freed on exit."""
+        w = dequantize_4bit(self.quantized, self.quant_state, dtype=dtype or self.quant_state.dtype)
+        prev, self._w_dense = self._w_dense, w
+        try:
+            yield w
+        finally:
+            self._w_dense = prev
+
+    def _linear(self, x: torch.Tensor, lora_a=None, lora_b=None, scaling: float = 1.0) -> torch.Tensor:
+        return nf4_linear(x, self.quantized, self.quant_state, self.bias, lora_a, lora_b, scaling,
+                          w_dense=self._w_dense, keep_weight_for_backward=self.keep_weight_for_backward)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return nf4_linear(x, self.quantized, self.quant_state, self.bias)
+        return self._linear(x)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, nf4 blocksize={self.quant_state.blocksize}"
@@ -196,12 +251,12 @@ class NF4LoRALinear(NF4Linear):
         nn.init.kaiming_uniform_(self.lora_A, a=math.sqrt(5))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return nf4_linear(x, self.quantized, self.quant_state, self.bias, self.lora_A, self.lora_B, self.scaling)
+        return self._linear(x, self.lora_A, self.lora_B, self.scaling)
 
 
 @torch.no_grad()
 def make_nf4_resident(module: nn.Module, device_id: int, *, lora_r: int = 0, lora_alpha: float = 16.0,
-                      lora_dtype: torch.dtype = torch.bfloat16) -> int:
+                      lora_dtype: torch.dtype = torch.bfloat16, exclude: Sequence[str] = ("lm_head",)) -> int:
     """Keep the staged NF4 weights of *module* packed on ``cuda:<device_id>``.
 
     Every ``nn.Linear`` inside *module* whose weight carries an NF4 payload
@@ -214,15 +269,20 @@ def make_nf4_resident(module: nn.Module, device_id: int, *, lora_r: int = 0, lor
     intended use; ``stratum/pipeline.py:906`` frees after the forward). The
     replacement keeps the payload (``.payload``) and the original bias; the
     staging calls (``ensure_weights`` / ``free_weights``) then find nothing to
-    do for these layers. Returns the number of layers replaced.
+    do for these layers. Layers whose attribute name is in ``exclude`` keep
+    the staged lifecycle: by default ``lm_head``, whose ``.weight`` the
+    reference's chunked loss reads directly (``stratum/model/chunked_loss.py:184``;
+    ``chunked_linear_cross_entropy`` of this package takes a swapped head).
+    Returns the number of layers replaced.
     """
     from .upload import NF4_ATTR  # local: upload imports this module's package
 
     device = torch.device("cuda", device_id)
+    skip = set(exclude)
     replaced = 0
     for parent in list(module.modules()):
         for name, child in list(parent.named_children()):
-            if type(child) is not nn.Linear or not hasattr(child.weight, NF4_ATTR):
+            if name in skip or type(child) is not nn.Linear or not hasattr(child.weight, NF4_ATTR):
                 continue
             payload = getattr(child.weight, NF4_ATTR)
             if len(payload.shape) != 2:

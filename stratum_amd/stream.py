@@ -28,8 +28,9 @@ drop-in for ``stratum.stage.DeviceStage`` (same constructor and
 
 from __future__ import annotations
 
+import sys
 from contextlib import nullcontext
-from typing import Any, Iterator, Optional, Sequence
+from typing import Any, Callable, Iterator, Optional, Sequence
 
 import torch
 import torch.nn as nn
@@ -41,11 +42,11 @@ class _LayerFeeder:
     """Materialises layers of a list on one device ahead of a consumer stream."""
 
     def __init__(self, layers: Sequence[nn.Module], device_id: int, lookahead: int,
-                 dequant_stream: "torch.cuda.Stream", consumer: "torch.cuda.Stream"):
+                 dequant_stream: "torch.cuda.Stream", consumers: Sequence["torch.cuda.Stream"]):
         if lookahead < 1:
             raise ValueError("lookahead must be >= 1")
         self.layers, self.device_id, self.lookahead = layers, device_id, lookahead
-        self.dequant_stream, self.consumer = dequant_stream, consumer
+        self.dequant_stream, self.consumers = dequant_stream, list(consumers)
         self.copies: dict = {}   # layer index -> NF4Prefetch in flight
         self.ready: dict = {}    # layer index -> event: materialised
 
@@ -57,7 +58,7 @@ class _LayerFeeder:
         if i in self.ready or not 0 <= i < len(self.layers):
             return
         self._copy(i)
-        readers = [self.consumer]
+        readers = self.consumers
         with torch.cuda.stream(self.dequant_stream):
             self.copies.pop(i).finalize(consumers=readers)
             ensure_weights(self.layers[i], self.device_id, consumers=readers)
@@ -79,7 +80,8 @@ class _LayerFeeder:
         self._materialise(i + 1)
         event = self.ready.pop(i)
         if event is not None:
-            self.consumer.wait_event(event)
+            for c in self.consumers:
+                c.wait_event(event)
 
 
 class NF4LayerStream:
@@ -110,7 +112,7 @@ class NF4LayerStream:
 
     def __iter__(self) -> Iterator[tuple[int, nn.Module]]:
         feeder = _LayerFeeder(self.layers, self.device_id, self.lookahead, self.dequant_stream,
-                              torch.cuda.current_stream(self.device_id))
+                              [torch.cuda.current_stream(self.device_id)])
         for i, layer in enumerate(self.layers):
             feeder.before(i)
             yield i, layer
@@ -131,10 +133,12 @@ class NF4DeviceStage(nn.Module):
     ``param_stream`` is the dequant stream, payload copies run on the device's
     copy stream ``lookahead`` layers ahead, and every tensor is handed over to
     the consuming stream. ``free_after_use=True`` frees each layer's staged
-    weights right after its forward is queued.
+    weights right after its forward is queued. ``recompute`` is the predicate
+    that labels a pass as recompute for ``iter_timer`` (see ``_action``).
     """
 
-    def __init__(self, layers: list, device_id: int, *, lookahead: int = 1, free_after_use: bool = False):
+    def __init__(self, layers: list, device_id: int, *, lookahead: int = 1, free_after_use: bool = False,
+                 recompute: Optional[Callable[[], bool]] = None):
         super().__init__()
         self.device_id = device_id
         self.layers = nn.ModuleList(layers)
@@ -142,6 +146,20 @@ class NF4DeviceStage(nn.Module):
         self.layer_start = 0
         self.lookahead = lookahead
         self.free_after_use = free_after_use
+        self.recompute = recompute
+
+    def _action(self) -> str:
+        """``"re"`` inside a recompute pass, else ``"fwd"`` -- the label the
+        reference gives ``iter_timer.time_fwd`` (``stratum/stage.py:123``), whose
+        scheduler keeps separate recompute estimates. The predicate is the
+        constructor's ``recompute``; without one, the ``doing_recompute`` of a
+        ``stratum.context`` module the host program has already loaded (this
+        package never imports it); with neither, every pass is a forward."""
+        pred = self.recompute
+        if pred is None:
+            ctx = sys.modules.get("stratum.context")
+            pred = getattr(ctx, "doing_recompute", None)
+        return "re" if pred is not None and pred() else "fwd"
 
     def set_timing_recorder(self, recorder, *, layer_start: int = 0) -> None:
         """Attach timing metadata for per-layer forward spans (``recorder.span``)."""
@@ -164,8 +182,14 @@ class NF4DeviceStage(nn.Module):
         run = [self.layers[i] for i in range(local_start, stop)]
         feeder = None
         if param_stream is not None and torch.cuda.is_available():
-            consumer = torch.cuda.current_stream(self.device_id)
-            feeder = _LayerFeeder(run, self.device_id, self.lookahead, param_stream, consumer)
+            # the stream that runs the layers waits on each layer's fence; so does
+            # the device's default stream when it is another one, as the reference
+            # fences the default stream (stratum/stage.py:121)
+            consumers = [torch.cuda.current_stream(self.device_id)]
+            default = torch.cuda.default_stream(self.device_id)
+            if default != consumers[0]:
+                consumers.append(default)
+            feeder = _LayerFeeder(run, self.device_id, self.lookahead, param_stream, consumers)
             if first_layer_fence is not None:
                 feeder.mark_ready(0, first_layer_fence)
         for k, layer in enumerate(run):
@@ -174,7 +198,7 @@ class NF4DeviceStage(nn.Module):
             stage_index = local_start + k
             timed = nullcontext()
             if iter_timer is not None and torch.cuda.is_available():
-                timed = iter_timer.time_fwd("fwd", self.layer_start + stage_index,
+                timed = iter_timer.time_fwd(self._action(), self.layer_start + stage_index,
                                             torch.cuda.current_stream(self.device_id))
             with timed, self._span(stage_device=self.device_id, layer_index=self.layer_start + stage_index,
                                    stage_layer_index=stage_index):

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version(L):
-    assert L.stm_nf4_abi_version() == 4
+    assert L.stm_nf4_abi_version() == 5
 
 
 @pytest.mark.parametrize("rule,code", [("argmin", 0), ("threshold", 1)])
@@ -339,6 +339,27 @@ def test_grouped_tile_rows_picks_the_fewest_padded_rows(L, counts, rows):
     off = np.zeros(len(counts) + 1, dtype=np.int32)
     off[1:] = np.cumsum(counts)
     assert L.stm_nf4_grouped_tile_rows(off.ctypes.data, len(counts)) == rows
+
+
+@pytest.mark.parametrize("offsets, max_rows, msg", [
+    ([0, 5, 3], 16, "decrease at expert 1"),
+    ([2, 5, 9], 16, "offsets[0] = 2"),
+    ([0, 5, 30], 16, "expert 1 has 25 rows, above max_rows 16"),
+    ([0, 0, -4], 16, "decrease at expert 1"),
+])
+def test_grouped_calls_refuse_bad_host_offsets_before_any_launch(L, offsets, max_rows, msg):
+    """Host offsets that break the contract (start at 0, never decrease, no
+    expert above max_rows) are refused by every grouped entry point before a
+    kernel is launched (these calls would otherwise need a GPU)."""
+    off = np.asarray(offsets, dtype=np.int32)
+    E = len(offsets) - 1
+    p = 4096  # a non-NULL, 256-byte aligned stand-in: never dereferenced
+    rc = L.stm_nf4_grouped_gemm_fwd(p, p, p, p, off.ctypes.data, E, max_rows, p, 64, 64, 64, 1, None)
+    assert rc == -1 and msg in _err(L)
+    rc = L.stm_nf4_grouped_gemm_bwd_dx(p, p, p, p, off.ctypes.data, E, max_rows, p, 64, 64, 64, 1, None)
+    assert rc == -1 and msg in _err(L)
+    if "max_rows" not in msg:  # the tile planner has no row bound
+        assert L.stm_nf4_grouped_tile_rows(off.ctypes.data, E) == -1 and msg in _err(L)
 
 
 def test_stack_nf4_equals_quantizing_the_stacked_weight():

@@ -109,3 +109,155 @@ def test_shape_mismatch_is_an_error(tmp_path):
     calls, fake = _stub_quantizer()
     with mock.patch.object(U, "quantize_4bit", fake), pytest.raises(ValueError, match="shape"):
         stream_load_and_quantize_module(Tiny(), str(tmp_path))
+
+
+# ---- checkpoint key mapping (stratum/upload.py:425-531): stage wrappers with a
+# layer index, PEFT base_layer, .inner./.layer. segments, tied lm_head, fused
+# expert banks, hub ids from the local cache
+
+
+class _Wrapped(nn.Module):
+    """A stage wrapper as the reference builds them: global layer index ``idx``
+    around the decoder layer ``layer``."""
+
+    def __init__(self, idx, inner):
+        super().__init__()
+        self.idx = idx
+        self.layer = inner
+
+
+class _Lora(nn.Module):
+    """PEFT's wrapper: the frozen Linear under ``base_layer``."""
+
+    def __init__(self, base):
+        super().__init__()
+        self.base_layer = base
+
+
+class _Decoder(nn.Module):
+    def __init__(self, experts=0):
+        super().__init__()
+        self.self_attn = nn.Module()
+        self.self_attn.q_proj = _Lora(nn.Linear(128, 64, bias=False, device="meta", dtype=torch.float16))
+        self.mlp = nn.Module()
+        self.mlp.inner = nn.Module()
+        self.mlp.inner.up_proj = nn.Linear(128, 64, bias=False, device="meta", dtype=torch.float16)
+        if experts:
+            self.feed_forward = nn.Module()
+            self.feed_forward.experts = nn.Module()
+            self.feed_forward.experts.gate_up_proj = nn.Parameter(
+                torch.empty(experts, 2 * 32, 64, device="meta", dtype=torch.float16))
+            self.feed_forward.experts.down_proj = nn.Parameter(
+                torch.empty(experts, 64, 32, device="meta", dtype=torch.float16))
+
+
+class _Stage(nn.Module):
+    def __init__(self, first, n, experts=0):
+        super().__init__()
+        self.layers = nn.ModuleList([_Wrapped(first + i, _Decoder(experts)) for i in range(n)])
+        for p in self.parameters():
+            p.requires_grad_(False)
+
+
+def _rand(shape, seed):
+    return (torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * 0.02).half()
+
+
+def test_key_function_order_and_variants():
+    keys = __import__("stratum_amd.checkpoint", fromlist=["x"]).checkpoint_key_fn(_Stage(7, 1))
+    ks = keys("layers.0.layer.mlp.inner.up_proj.weight")
+    assert ks[0] == "layers.0.layer.mlp.inner.up_proj.weight"           # the name itself first
+    assert "model.layers.7.mlp.up_proj.weight" in ks                      # global index, .inner. dropped
+    assert "model.layers.7.mlp.inner.up_proj.weight" in ks
+    assert len(ks) == len(set(ks))
+    q = keys("layers.0.layer.self_attn.q_proj.base_layer.weight")
+    assert "model.layers.7.self_attn.q_proj.weight" in q and q.index("model.layers.7.self_attn.q_proj.weight") > 0
+    assert keys("layers.0.module.layer.mlp.inner.up_proj.weight")[0] == "layers.0.layer.mlp.inner.up_proj.weight"
+    # the plain spellings come before the model.-prefixed ones of the same name
+    plain = keys("norm.weight")
+    assert plain.index("norm.weight") < plain.index("model.norm.weight")
+    tied = keys("lm_head.weight")
+    assert tied[0] == "lm_head.weight" and "model.embed_tokens.weight" in tied and "embed_tokens.weight" in tied
+
+
+@pytest.mark.parametrize("sharded", [False, True])
+def test_stage_local_wrapped_layers_load_their_global_keys(tmp_path, sharded):
+    ck = tmp_path / "ck"
+    ck.mkdir()
+    t = {}
+    for g in (4, 5):
+        t[f"model.layers.{g}.self_attn.q_proj.weight"] = _rand((64, 128), g)
+        t[f"model.layers.{g}.mlp.up_proj.weight"] = _rand((64, 128), 10 + g)
+    _write(ck, t, sharded)
+    calls, fake = _stub_quantizer()
+    stage = _Stage(4, 2)
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        stats = stream_load_and_quantize_module(stage, str(ck), min_numel=4096)
+    assert stats is not None and stats.tensors == 4 and len(calls) == 4
+    # small enough to stay dense: the values are the global layer's
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        stage2 = _Stage(4, 2)
+        stats2 = stream_load_and_quantize_module(stage2, str(ck), min_numel=1 << 20)
+    assert stats2 is not None and stats2.tensors == 0
+    assert torch.equal(stage2.layers[1].layer.self_attn.q_proj.base_layer.weight, t["model.layers.5.self_attn.q_proj.weight"])
+    assert torch.equal(stage2.layers[0].layer.mlp.inner.up_proj.weight, t["model.layers.4.mlp.up_proj.weight"])
+
+
+def test_tied_lm_head_reads_the_embedding(tmp_path):
+    class Postfix(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.lm_head = nn.Linear(128, 256, bias=False, device="meta", dtype=torch.float16)
+            self.lm_head.weight.requires_grad_(False)
+
+    emb = _rand((256, 128), 3)
+    save_file({"model.embed_tokens.weight": emb}, str(tmp_path / "model.safetensors"))
+    calls, fake = _stub_quantizer()
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        m = Postfix()
+        assert stream_load_and_quantize_module(m, str(tmp_path), min_numel=1 << 20).tensors == 0
+    assert torch.equal(m.lm_head.weight, emb)
+
+
+def test_fused_expert_banks_stack_per_expert_tensors(tmp_path):
+    E = 3
+    t = {f"model.layers.2.self_attn.q_proj.weight": _rand((64, 128), 1),
+         f"model.layers.2.mlp.up_proj.weight": _rand((64, 128), 2)}
+    for e in range(E):
+        t[f"model.layers.2.feed_forward.experts.{e}.w1.weight"] = _rand((32, 64), 100 + e)
+        t[f"model.layers.2.feed_forward.experts.{e}.w3.weight"] = _rand((32, 64), 200 + e)
+        t[f"model.layers.2.feed_forward.experts.{e}.w2.weight"] = _rand((64, 32), 300 + e)
+    _write(tmp_path, t, True)
+    calls, fake = _stub_quantizer()
+    stage = _Stage(2, 1, experts=E)
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        stats = stream_load_and_quantize_module(stage, str(tmp_path), min_numel=1 << 20)
+    assert stats is not None
+    ex = stage.layers[0].layer.feed_forward.experts
+    want_gu = torch.stack([torch.cat([t[f"model.layers.2.feed_forward.experts.{e}.w1.weight"],
+                                      t[f"model.layers.2.feed_forward.experts.{e}.w3.weight"]]) for e in range(E)])
+    want_d = torch.stack([t[f"model.layers.2.feed_forward.experts.{e}.w2.weight"] for e in range(E)])
+    assert torch.equal(ex.gate_up_proj, want_gu) and torch.equal(ex.down_proj, want_d)
+    # a missing expert: no bank, no key -> None
+    del t["model.layers.2.feed_forward.experts.1.w2.weight"]
+    (tmp_path / "b").mkdir()
+    _write(tmp_path / "b", t, False)
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        assert stream_load_and_quantize_module(_Stage(2, 1, experts=E), str(tmp_path / "b"), min_numel=1 << 20) is None
+
+
+def test_hub_id_resolves_through_the_local_cache_only(tmp_path, monkeypatch):
+    import huggingface_hub.constants as C
+    snap = tmp_path / "hub" / "models--org--tiny" / "snapshots" / "abc123"
+    snap.mkdir(parents=True)
+    (tmp_path / "hub" / "models--org--tiny" / "refs").mkdir()
+    (tmp_path / "hub" / "models--org--tiny" / "refs" / "main").write_text("abc123")
+    _write(snap, _tensors(), False)
+    monkeypatch.setattr(C, "HF_HUB_CACHE", str(tmp_path / "hub"))
+    monkeypatch.setenv("HF_HUB_OFFLINE", "1")
+    calls, fake = _stub_quantizer()
+    with mock.patch.object(U, "quantize_4bit", fake), mock.patch.object(U, "_pin_cpu", lambda x: x):
+        m = Tiny()
+        stats = stream_load_and_quantize_module(m, "org/tiny", min_numel=4096)
+        assert stats is not None and stats.tensors == 1
+        assert stream_load_and_quantize_module(Tiny(), "org/absent", min_numel=4096) is None

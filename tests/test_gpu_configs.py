@@ -218,3 +218,70 @@ def test_8b_layers_stream_in_bit_exact_at_every_yield(cuda):
         for name in LAYER_8B:
             wt = getattr(layer, name).weight
             assert wt.data.numel() == 0 and hasattr(wt, NF4_ATTR)
+
+
+# ----------------------------------------- LoRA step, W [14336, 4096], M = 8192
+LORA_STEP = (8192, 14336, 4096, 16)  # M, N, K, rank (r = 16, alpha = 16: scaling 1)
+
+
+@pytest.fixture(scope="module")
+def lora_step(cuda):
+    """The LoRA-step workload: W [14336, 4096] N(0, 0.02) fp16 -> NF4, X bf16
+    [8192, 4096] N(0, 1), dY bf16 N(0, 1); oracle codes and bf16 weight."""
+    M, N, K, R = LORA_STEP
+    rp, ra, wq = oracle_weight(seeded((N, K), 55, 0.02, torch.float16), torch.bfloat16)
+    return dict(q=torch.from_numpy(rp).to(cuda), a=torch.from_numpy(ra).to(cuda), w=wq.to(cuda).float(),
+                x=seeded((M, K), 1, 1.0, torch.bfloat16).to(cuda), dy=seeded((M, N), 2, 1.0, torch.bfloat16).to(cuda))
+
+
+@pytest.mark.parametrize("lora_std", [0.01, 0.1])
+def test_lora_step_fused_kernels_with_lora_terms(cuda, lora_step, lora_std):
+    """Forward with the rank-16 epilogue (T . B^T) and input gradient with the
+    U . A term, at the full LoRA-step size, whole matrix and every 32 x 32
+    fragment against fp32 on the oracle weight. A, B ~ N(0, 0.01) is the
+    workload's init; at 0.1 the LoRA term is as large as the base product, so
+    a wrong or dropped epilogue fails the bar everywhere."""
+    from stratum_amd.functional import lora_down, lora_dy, nf4_gemm_bwd_dx, nf4_gemm_fwd
+    M, N, K, R = LORA_STEP
+    s = lora_step
+    A = seeded((R, K), 10, lora_std, torch.bfloat16).to(cuda)
+    B = seeded((N, R), 11, lora_std, torch.bfloat16).to(cuda)
+    t = lora_down(s["x"], A, 1.0)
+    y = nf4_gemm_fwd(s["x"], s["q"], s["a"], (N, K), 64, lora_t=t, lora_b=B)
+    ref = s["x"].float() @ s["w"].t().contiguous() + t.float() @ B.float().t().contiguous()
+    assert_gemm_close(y, ref, torch.bfloat16, "forward with LoRA epilogue")
+    del y, ref
+    u, _ = lora_dy(s["dy"], B, None, 1.0)
+    dx = nf4_gemm_bwd_dx(s["dy"], s["q"], s["a"], (N, K), 64, lora_u=u, lora_at=A.t().contiguous())
+    ref = s["dy"].float() @ s["w"] + u.float() @ A.float()
+    assert_gemm_close(dx, ref, torch.bfloat16, "input gradient with U . A")
+
+
+def test_lora_step_forced_fused_module_step(cuda, lora_step, monkeypatch):
+    """The step bench.py times: NF4LoRALinear forward and backward with the fused
+    kernels forced at 8192 rows -- y, dX, dA and dB against fp32 autograd on the
+    oracle weight (whole matrix and per fragment)."""
+    from stratum_amd.functional import QuantState
+    from stratum_amd.nf4_linear import NF4LoRALinear
+    monkeypatch.setenv("STRATUM_NF4_FUSED_MAX_ROWS", "-1")
+    M, N, K, R = LORA_STEP
+    s = lora_step
+    st = QuantState(absmax=s["a"], shape=(N, K), blocksize=64, dtype=torch.bfloat16)
+    lin = NF4LoRALinear(s["q"], st, r=R, lora_alpha=16.0)
+    with torch.no_grad():
+        lin.lora_A.copy_(seeded((R, K), 10, 0.1, torch.bfloat16))
+        lin.lora_B.copy_(seeded((N, R), 11, 0.1, torch.bfloat16))
+    x = s["x"].clone().requires_grad_(True)
+    y = lin(x)
+    y.backward(s["dy"])
+    torch.cuda.synchronize()
+    xr = s["x"].float().requires_grad_(True)
+    Ar = lin.lora_A.detach().float().requires_grad_(True)
+    Br = lin.lora_B.detach().float().requires_grad_(True)
+    yr = xr @ s["w"].t().contiguous() + (xr @ Ar.t().contiguous()) @ Br.t().contiguous()
+    yr.backward(s["dy"].float())
+    assert_gemm_close(y.detach(), yr.detach(), torch.bfloat16, "module forward")
+    del y, yr
+    assert_gemm_close(x.grad, xr.grad, torch.bfloat16, "module dX")
+    assert_gemm_close(lin.lora_A.grad, Ar.grad, torch.bfloat16, "dA")
+    assert_gemm_close(lin.lora_B.grad, Br.grad, torch.bfloat16, "dB")

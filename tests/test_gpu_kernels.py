@@ -106,6 +106,27 @@ def test_quantize_special_blocks_bit_exact(cuda, rule, dtype):
     np.testing.assert_array_equal(got[~np.isnan(got)].view(np.uint32), ref_a[~np.isnan(ref_a)].view(np.uint32))
 
 
+@pytest.mark.parametrize("rule", ["argmin", "threshold"])
+@pytest.mark.parametrize("n", [64 * 64, 64 * 9 + 37])  # whole blocks; a partial block (one-thread kernel)
+def test_quantize_fp32_nan_payloads_give_code_zero(cuda, rule, n):
+    """fp32 NaNs whose payload bits fall in the kernel's cell-index bits
+    (quiet and signalling, both signs): their blocks quantize to code 0 with a
+    NaN absmax, bit-exact against the oracle, and the other blocks are intact."""
+    from stratum_amd.functional import quantize_4bit
+    x = seeded((n,), 31, 1.0, torch.float32)
+    bits = x.view(torch.int32)
+    payloads = [0x7FC003FC, 0x7FC00004, 0x7FC00100, 0xFFC003F8, 0x7F8003FF, 0xFF800201, 0x7FFFFFFF]
+    for i, pl in enumerate(payloads):
+        pos = (2 * i) * 64 + 5 * i + 1 if (2 * i) * 64 + 5 * i + 1 < n else n - 1 - i
+        bits[pos] = torch.tensor(pl, dtype=torch.int64).to(torch.int32)  # wraps to the signed value
+    packed, state = quantize_4bit(x.to(cuda), blocksize=64, rounding=rule)
+    ref_p, ref_a = oracle_quant(x, 64, rule)
+    np.testing.assert_array_equal(packed.cpu().numpy().ravel(), ref_p)
+    got = state.absmax.cpu().numpy()
+    assert np.isnan(ref_a).sum() >= 4 and np.array_equal(np.isnan(got), np.isnan(ref_a))
+    np.testing.assert_array_equal(got[~np.isnan(got)].view(np.uint32), ref_a[~np.isnan(ref_a)].view(np.uint32))
+
+
 def test_quantize_unaligned_input_and_cpu_input(cuda):
     from stratum_amd import _lib
     from stratum_amd.functional import quantize_4bit
