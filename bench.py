@@ -194,6 +194,45 @@ def _cpu_model():
     return "unknown"
 
 
+def _forced_fused(fn):
+    """fn() with the fused kernels forced at every row count."""
+    policy = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
+    os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = "-1"
+    try:
+        return fn()
+    finally:
+        if policy is None:
+            del os.environ["STRATUM_NF4_FUSED_MAX_ROWS"]
+        else:
+            os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = policy
+
+
+def check_step_output(torch, step_once, x, A, B, dy, w):
+    """One untimed run of the timed step, its y, dX, dA and dB against fp32
+    torch on the dequantized weight (relative Frobenius error, bf16 bar 1e-2).
+    Raises if any is off: a throughput of wrong results is not reported."""
+    x.grad = A.grad = B.grad = None
+    y = step_once()
+    y.backward(dy)
+    got = {"y": y.detach(), "dX": x.grad, "dA": A.grad, "dB": B.grad}
+    xr = x.detach().float().requires_grad_(True)
+    Ar = A.detach().float().requires_grad_(True)
+    Br = B.detach().float().requires_grad_(True)
+    yr = xr @ w.float().t().contiguous() + (xr @ Ar.t().contiguous()) @ Br.t().contiguous()
+    yr.backward(dy.float())
+    ref = {"y": yr.detach(), "dX": xr.grad, "dA": Ar.grad, "dB": Br.grad}
+    rel = {k: ((got[k].float() - ref[k]).norm() / ref[k].norm()).item() for k in got}
+    x.grad = A.grad = B.grad = None
+    del y, yr, got, ref
+    torch.cuda.empty_cache()
+    bad = {k: v for k, v in rel.items() if not v <= 1e-2}
+    if bad:
+        raise SystemExit(f"bench: the timed step's output is off the fp32 reference: {bad}")
+    return {"rel_err": {k: float(f"{v:.3e}") for k, v in rel.items()}, "tol": 1e-2,
+            "what": "one untimed run of the timed step (fused kernels forced) against fp32 torch on the "
+                    "dequantized weight"}
+
+
 def run_lora_step(args):
     import torch
 
@@ -279,6 +318,9 @@ def run_lora_step(args):
     torch.cuda.synchronize()
     ref_ms = (time.perf_counter() - t0) * 1e3 / side_steps
     ms = elapsed * 1e3 / args.steps
+    output_check = check_step_output(torch, step_once=lambda: _forced_fused(lambda: nf4_linear(x, packed, state, None,
+                                                                                               A, B, 1.0)),
+                                     x=x, A=A, B=B, dy=dy, w=dequantize_4bit(packed, state))
     base_flops = 2 * 2.0 * M * N * K
     lora_flops = 2.0 * M * K * R + 2.0 * M * R * N           # forward rank-16 path
     lora_flops += 2.0 * M * N * R + 2.0 * M * R * K          # dX rank-16 term
@@ -346,6 +388,8 @@ def run_lora_step(args):
         "roofline": {"bound": "mfma", "kernel": "k_gemm_fwd_rw<BF16>", "achieved": round(fwd_tf, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd_rw"),
+                     "traffic_source": "profiles/traffic_lora_step_w14336x4096_x8192.json (rocprofv3 "
+                                       "FETCH_SIZE + WRITE_SIZE per launch, calibrated; not measured in this run)",
                      "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
         "bwd_dx": {"kernel": "k_gemm_bwd_rw<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
@@ -355,8 +399,9 @@ def run_lora_step(args):
                     "traffic": traffic.get("k_dequantize")},
         "unfused_fwd": {"what": "dequantize kernel + torch.matmul (hipBLASLt)",
                         "tflops": round(gemm_flops / (unf_ms * 1e-3) / 1e12, 2), "ms": round(unf_ms, 4)},
+        "output_check": output_check,
         "default_policy_step": {"what": "NF4LoRALinear default above 1024 rows: dequantize + hipBLASLt, "
-                                        "backward re-dequantizes",
+                                        "the backward reuses the forward's dequantized temporary",
                                 "ms_per_step": round(default_ms, 4),
                                 "tflops": round(base_flops / (default_ms * 1e-3) / 1e12, 2)},
         "reference_architecture_step": {"what": "dequantize for the forward and again for the backward, torch "

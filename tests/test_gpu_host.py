@@ -258,7 +258,8 @@ def test_nf4_linear_default_policy_by_rows(cuda, monkeypatch):
     wq = oracle_weight(w, torch.bfloat16, cuda)
     calls = []
     real = NL._NF4LinearFn.apply
-    monkeypatch.setattr(NL._NF4LinearFn, "apply", lambda *a: calls.append(a[-1]) or real(*a))
+    # argument 9 of _NF4LinearFn.apply is the fused flag
+    monkeypatch.setattr(NL._NF4LinearFn, "apply", lambda *a: calls.append(a[9]) or real(*a))
     for M in (768, 769):
         x = seeded((M, K), 22, 1.0, torch.bfloat16).to(cuda)
         y = NL.NF4Linear(q, st)(x)
