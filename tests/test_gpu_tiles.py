@@ -120,6 +120,9 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (24, 520, 576, 64, True, 16),      # 32-row variant, split, LoRA in the reduce
     (31, 200, 448, 64, True, 0),       # 32-row variant, blocks of 192 rows (second partial), K % 256 == 192
     (32, 4104, 4160, 64, False, 16),   # 32-row variant, uneven ranges
+    (320, 520, 576, 64, True, 16),     # last 256-row tile: 64 rows (the 2-fragment short item)
+    (384, 264, 640, 64, False, 0),     # last 256-row tile: 128 rows (the 4-fragment short item)
+    (100, 256, 1024, 128, True, 16),   # one tile of 100 rows (4 fragments), blocksize 128
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
@@ -154,6 +157,9 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
     (300, 512, 384, 128, 32),          # blocksize 128, second tile 128 wide
     (64, 128, 960, 64, 16),            # last tile 192 wide
     (33, 4096, 2048, 64, 0),           # small M: split reductions exist
+    (320, 512, 576, 64, 16),           # last 256-row tile: 64 rows (the 2-fragment short item)
+    (384, 256, 640, 64, 0),            # last 256-row tile: 128 rows (the 4-fragment short item)
+    (100, 1024, 256, 128, 16),         # one tile of 100 rows (4 fragments), blocksize 128
 ])
 def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
     from stratum_amd import _lib
