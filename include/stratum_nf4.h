@@ -195,8 +195,9 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
 
 /*
  * Tile height (192 or 256 rows) the grouped forward uses for these row counts
- * (host int32 [E + 1] offsets): the height that computes the fewest padded
- * rows, a 192-row tile's row weighted 8 % dearer. Pure host function; no
+ * (host int32 [E + 1] offsets): the cheaper by a per-item cost model (a full
+ * 256-row item 1, an expert's last 256-row item 0.45 / 0.6 when it holds at
+ * most 64 / 128 rows, a 192-row item 0.81). Pure host function; no
  * counterpart in the reference (its per-expert loop has no tiles).
  * Returns 192, 256, or STM_ERR_INVALID (NULL, num_experts <= 0, offsets[0] != 0
  * or decreasing offsets).

@@ -158,10 +158,11 @@ __device__ __forceinline__ Group group_of(const GemmArgs& g, int e) {
 // GROUP_M = 4 runs 4 activation x 8 weight tiles together; measured at
 // M = 8192 on W [14336, 4096] it fetches 735 MB per forward from beyond L2
 // (GROUP_M = 8: 1072 MB, 2: 820 MB) and is 1-4 % faster.
-__device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn,
+                                            bool xcd_runs = true) {
     const int64_t T = ntm * ntn;
     const int64_t T8 = (T / 8) * 8;
-    if (pid < T8) pid = (pid % 8) * (T / 8) + pid / 8;
+    if (xcd_runs && pid < T8) pid = (pid % 8) * (T / 8) + pid / 8;
     const int64_t per_group = (int64_t)STM_GROUP_M * ntn;
     const int64_t grp = pid / per_group;
     const int64_t first = grp * STM_GROUP_M;
@@ -169,6 +170,18 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t ntm, int64_t nt
     const int64_t in = pid % per_group;
     tm = first + in % gsize;
     tn = in / gsize;
+}
+
+// Grouped launches (experts): item w of a work-group runs on XCD w % 8, so the
+// item list (expert-major: an expert's tiles are consecutive) is cut into 8
+// contiguous runs, one per XCD. An expert's tiles then run together on one XCD
+// and share its rows of the activations (and the expert's weight) in that
+// XCD's L2, instead of being spread over all eight. Dense launches keep the
+// per-tile order of tile_coords. A bijection on [0, work).
+__device__ __forceinline__ int64_t item_order(int64_t w, int64_t work, int num_groups) {
+    if (num_groups <= 1) return w;
+    const int64_t W8 = (work / 8) * 8;
+    return w < W8 ? (w % 8) * (work / 8) + w / 8 : w;
 }
 
 // Activation staging: the tile rows [m0, m0 + BM) x [k0, k0 + 64) are copied
@@ -626,11 +639,12 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_fwd(GemmArgs g) {
     // fills the level table once and overlaps one item's stores with the next
     // item's first loads).
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
-    const int64_t rest = w / tiles;
+    const int64_t wi = item_order(w, work, g.num_groups);
+    const int64_t rest = wi / tiles;
     const int z = (int)(rest / g.num_groups);
     const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tn;
-    tile_coords(w % tiles, ntm, ntn, tm, tn);
+    tile_coords(wi % tiles, ntm, ntn, tm, tn, g.num_groups == 1);
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) continue;  // uniform over the work-group
 
@@ -728,11 +742,16 @@ struct RwWeights {
     uint32_t copy_off;     // 8 * (lane % 32)
 
     __device__ __forceinline__ void load(int64_t k0, Raw& r) const {
+        load_words(k0, r);
+        load_absmax(k0, r);
+    }
+    __device__ __forceinline__ void load_words(int64_t k0, Raw& r) const {
 #pragma unroll
-        for (int i = 0; i < FA; ++i) {
-            r.q[i] = *reinterpret_cast<const uint4*>(packed + (woff[i] + (uint32_t)(k0 / 2)));
-            r.a[i] = absmax[aoff[i] + (uint32_t)((kbase + k0) >> bshift)];
-        }
+        for (int i = 0; i < FA; ++i) r.q[i] = *reinterpret_cast<const uint4*>(packed + (woff[i] + (uint32_t)(k0 / 2)));
+    }
+    __device__ __forceinline__ void load_absmax(int64_t k0, Raw& r) const {
+#pragma unroll
+        for (int i = 0; i < FA; ++i) r.a[i] = absmax[aoff[i] + (uint32_t)((kbase + k0) >> bshift)];
     }
     __device__ __forceinline__ static uint32_t word(const uint4& q, int j) {
         return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
@@ -751,9 +770,13 @@ struct RwWeights {
         }
     }
     __device__ __forceinline__ static void finish(const Raw& r, const f32x2_t (&p)[FA][4], uint4 (&out)[FA]) {
+        finish_a(r.a, p, out);
+    }
+    __device__ __forceinline__ static void finish_a(const float (&am)[FA], const f32x2_t (&p)[FA][4],
+                                                    uint4 (&out)[FA]) {
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
-            const float a = r.a[i];
+            const float a = am[i];
             out[i].x = Tr::pack2(opaque(p[i][0].x * a), opaque(p[i][0].y * a));
             out[i].y = Tr::pack2(opaque(p[i][1].x * a), opaque(p[i][1].y * a));
             out[i].z = Tr::pack2(opaque(p[i][2].x * a), opaque(p[i][2].y * a));
@@ -886,6 +909,14 @@ __device__ __forceinline__ void rw_slot_pattern() {
     }
 }
 
+// 1: the forward register-weight kernel issues each step's loads right after
+// the barrier that frees their destination (a whole step to land); 0: the
+// activation copy at the start of the step and the weight loads after its
+// first sub-step.
+#ifndef STM_RW_EARLY_LOADS
+#define STM_RW_EARLY_LOADS 1
+#endif
+
 // Items with at most 64 / 128 valid rows run the 256-row register-weight
 // kernels' main loop over 2 / 4 of the 8 row fragments (1: on).
 #ifndef STM_SHORT_ITEMS
@@ -907,11 +938,12 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
     const int64_t work = tiles * g.num_groups * g.splits;
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items (tile, expert, split) as in k_gemm_fwd
-    const int64_t rest = w / tiles;
+    const int64_t wi = item_order(w, work, g.num_groups);
+    const int64_t rest = wi / tiles;
     const int z = (int)(rest / g.num_groups);
     const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tn;
-    tile_coords(w % tiles, ntm, ntn, tm, tn);
+    tile_coords(wi % tiles, ntm, ntn, tm, tn, g.num_groups == 1);
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) continue;
 
@@ -956,6 +988,79 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     // (64 or 128 rows): a quarter or half of the MFMAs, the same weight work,
     // and only the waves whose rows hold them copy activations. Rows past the
     // valid ones are never stored.
+#if STM_RW_EARLY_LOADS
+    // The activation tile of step s + 2 and the packed words of step s + 3 are
+    // issued right after the barrier that frees their destination (the buffer
+    // step s has just released; the words of step s + 1, whose last table reads
+    // go out first), so they have a whole step to land before the next
+    // step-end wait (vmcnt(0) counts every load in flight). A step's absmax is
+    // loaded, as before, once the absmax it replaces has been used (after
+    // sub-step 0). Every load writes the registers the loop carries: no copies.
+    auto main_loop = [&](auto fba_tag) {
+        constexpr int FBA = decltype(fba_tag)::value;
+        // wave w copies the activation rows [w R, w R + R), R = BM / (4 WM)
+        const bool copies = FBA == FB || wave * (BM / (4 * WM)) < 32 * FBA;
+
+        // prologue: activation tiles 0 and 1, packed weights of steps 0 and 1;
+        // fragments of sub-steps 0..2 of step 0, table reads of its sub-step 3;
+        // then step 2's packed words into step 0's registers
+        ws.load(0, raw0);
+        ws.load(KT > 1 ? BK : 0, raw1);
+        if (copies) {
+            as.issue(0, 0);
+            as.issue(KT > 1 ? BK : 0, 1);
+        }
+        wait_vmem();
+        __syncthreads();  // level table and activation tiles 0 and 1 ready
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            ws.issue(raw0, j, pa);
+            RwWeights<Tr>::finish(raw0, pa, B[j]);
+        }
+        ws.issue(raw0, 3, pa);
+        ws.load_words((KT > 2 ? 2 : KT - 1) * (int64_t)BK, raw0);
+        read_x<FB, FBA>(x, sA0, xrow0, lane, 0);
+        sched_fence();
+
+        auto sub = [&](const uint4 (&w)[2], const uint4* sx, int jn, const typename RwWeights<Tr>::Raw& r_next,
+                       int word_next, f32x2_t (&p_next)[2][4], const typename RwWeights<Tr>::Raw& r_cur,
+                       const f32x2_t (&p_cur)[2][4], uint4 (&bout)[2]) {
+            ws.issue(r_next, word_next, p_next);
+            mma_sub<Tr, 2, FB, FBA>(acc, w, x, sx, xrow0, lane, jn);
+            RwWeights<Tr>::finish(r_cur, p_cur, bout);
+            rw_slot_pattern<2 * FBA>();
+            sched_fence();
+        };
+
+        // step s: rawc = (packed words of step s + 2, in flight; absmax of step
+        // s), rawn = step s + 1; activation tile s in sAc, s + 1 in sAn (in flight)
+        auto step = [&](int s, const uint4* sAc, const uint4* sAn, int cbuf, typename RwWeights<Tr>::Raw& rawc,
+                        typename RwWeights<Tr>::Raw& rawn) {
+            const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+            const int s3 = s + 3 < KT ? s + 3 : KT - 1;
+            sub(B[0], sAc, 1, rawn, 0, pb, rawc, pa, B[3]);
+            ws.load_absmax((int64_t)s2 * BK, rawc);
+            sub(B[1], sAc, 2, rawn, 1, pa, rawn, pb, B[0]);
+            sub(B[2], sAc, 3, rawn, 2, pb, rawn, pa, B[1]);
+            wait_vmem();
+            __syncthreads();  // tile s + 1 in sAn; sAc released by every wave
+            if (copies) as.issue((int64_t)s2 * BK, cbuf);
+            ws.issue(rawn, 3, pa);
+            ws.load_words((int64_t)s3 * BK, rawn);
+            mma_sub<Tr, 2, FB, FBA>(acc, B[3], x, sAn, xrow0, lane, 0);
+            RwWeights<Tr>::finish(rawn, pb, B[2]);
+            rw_slot_pattern<2 * FBA>();
+            sched_fence();
+        };
+        int s = 0;
+        for (; s + 1 < KT; s += 2) {
+            step(s, sA0, sA1, 0, raw0, raw1);
+            step(s + 1, sA1, sA0, 1, raw1, raw0);
+        }
+        if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
+        wait_vmem();  // the loads past the last step (clamped to it) land before the epilogue reuses LDS
+    };
+#else
     auto main_loop = [&](auto fba_tag) {
         constexpr int FBA = decltype(fba_tag)::value;
         // wave w copies the activation rows [w R, w R + R), R = BM / (4 WM)
@@ -1012,6 +1117,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
         }
         if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
     };
+#endif
     // the item's valid rows decide (uniform over the work-group, so every wave
     // takes the same branch and meets the same barriers)
     const int64_t valid = grp.rows - m0;
@@ -1096,11 +1202,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fwd_r8(GemmArgs g) {
     const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
     const int64_t work = tiles * g.num_groups * g.splits;
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
-    const int64_t rest = w / tiles;
+    const int64_t wi = item_order(w, work, g.num_groups);
+    const int64_t rest = wi / tiles;
     const int z = (int)(rest / g.num_groups);
     const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tn;
-    tile_coords(w % tiles, ntm, ntn, tm, tn);
+    tile_coords(wi % tiles, ntm, ntn, tm, tn, g.num_groups == 1);
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) continue;
 
@@ -1294,11 +1401,12 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_bwd(GemmArgs g) {
     const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
     const int64_t work = tiles * g.num_groups * g.splits;
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items as in k_gemm_fwd
-    const int64_t rest = w / tiles;
+    const int64_t wi = item_order(w, work, g.num_groups);
+    const int64_t rest = wi / tiles;
     const int z = (int)(rest / g.num_groups);
     const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tk;
-    tile_coords(w % tiles, ntm, ntk, tm, tk);
+    tile_coords(wi % tiles, ntm, ntk, tm, tk, g.num_groups == 1);
     const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) continue;
 
@@ -1432,11 +1540,12 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
     const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
     const int64_t work = tiles * g.num_groups * g.splits;
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // items (tile, expert, split)
-    const int64_t rest = w / tiles;
+    const int64_t wi = item_order(w, work, g.num_groups);
+    const int64_t rest = wi / tiles;
     const int z = (int)(rest / g.num_groups);
     const Group grp = group_of(g, (int)(rest % g.num_groups));
     int64_t tm, tk;
-    tile_coords(w % tiles, ntm, ntk, tm, tk);
+    tile_coords(wi % tiles, ntm, ntk, tm, tk, g.num_groups == 1);
     const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) continue;
 
@@ -1514,6 +1623,99 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
     const int xh = lane >> 5;
     auto xch = [&](int j) { return 4 * (j >> 1) + 2 * xh + (j & 1); };
 
+#if STM_RW_EARLY_LOADS
+    // The main loop over the first FBA row fragments (as in k_gemm_fwd_rw: an
+    // item with at most 64 / 128 valid rows runs 2 / 4 of them, and only the
+    // waves whose rows hold them copy dY). Each step's loads are issued right
+    // after the barrier that frees their destination, so each has a whole step
+    // to land before the next step-end wait: dY of step s + 2 into the dY buffer
+    // step s has released, the packed tile of step s + 3 into the tile buffer
+    // whose tile (s + 1) was read into registers a barrier ago, and the absmax
+    // of step s + 3 into a register, stored to its LDS buffer before the next
+    // barrier.
+    auto main_loop = [&](auto fba_tag) {
+        constexpr int FBA = decltype(fba_tag)::value;
+        // wave w copies the dY rows [w BM / 4, (w + 1) BM / 4)
+        const bool copies = FBA == FB || wave * (BM / 4) < 32 * FBA;
+
+        // prologue: dY(0) and dY(1), packed tiles of steps 0 and 1, absmax of
+        // steps 0 and 1; fragments of sub-steps 0..2 of step 0, table reads of its
+        // sub-step 3; then the tile and absmax of step 2
+        {
+            const float a0 = load_abs(0), a1 = load_abs(KT > 1 ? 1 : 0);
+            if (copies) {
+                as.issue(0, 0);
+                as.issue(KT > 1 ? BK : 0, 1);
+            }
+            copy_w(0, 0);
+            copy_w(KT > 1 ? 1 : 0, 1);
+            wait_vmem();
+            store_abs(0, a0);
+            store_abs(1, a1);  // absmax of step s in buffer s % 3
+        }
+        __syncthreads();  // level table, dY(0), dY(1), tiles 0 and 1, absmax 0 and 1 ready
+        RwWeightsT<Tr>::read(tile0, traddr, raw0);
+        RwWeightsT<Tr>::read(tile1, traddr, raw1);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            ws.issue(raw0, j, pa, absrow(0, j), aa);
+            RwWeightsT<Tr>::finish(pa, aa, B[j]);
+        }
+        ws.issue(raw0, 3, pa, absrow(0, 3), aa);
+        // activation fragments of sub-step 0
+#pragma unroll
+        for (int f = 0; f < FBA; ++f) x[f] = sA0[swz(f * 32 + (lane & 31), xch(0))];
+        __syncthreads();  // every wave has read tile 0 before its buffer takes tile 2
+        copy_w(KT > 2 ? 2 : KT - 1, 0);
+        float a_next = load_abs(KT > 2 ? 2 : KT - 1);
+
+        auto sub = [&](const uint4 (&wf)[2], const uint4* sx, int jn, const typename RwWeightsT<Tr>::Raw& r_next,
+                       int j_next, uint32_t arow_next, f32x2_t (&p_next)[2][4], f32x4_t (&a_next)[2],
+                       const f32x2_t (&p_cur)[2][4], const f32x4_t (&a_cur)[2], uint4 (&bout)[2]) {
+            ws.issue(r_next, j_next, p_next, arow_next, a_next);
+            const int ch = xch(jn);
+#pragma unroll
+            for (int f = 0; f < FBA; ++f) {
+                acc[0][f] = mfma<Tr>(wf[0], x[f], acc[0][f]);
+                acc[1][f] = mfma<Tr>(wf[1], x[f], acc[1][f]);
+                x[f] = sx[swz(f * 32 + (lane & 31), ch)];
+            }
+            RwWeightsT<Tr>::finish(p_cur, a_cur, bout);
+            rw_slot_pattern<2 * FBA>();
+            sched_fence();
+        };
+
+        // step s: rawc = transposed tile of step s (its sub-step 3 not yet made),
+        // rawn = step s + 1; dY(s) in sAc, dY(s + 1) in sAn (in flight); tile s + 2
+        // in flight into buffer cur; a_next = absmax of step s + 2 (in flight);
+        // absmax buffers rotate over three (step s + 1 in a1, step s + 2 into
+        // a2buf, whose last reader, step s - 2's sub-step 3, is a barrier behind)
+        auto step = [&](int s, const uint4* sAc, const uint4* sAn, int cur, typename RwWeightsT<Tr>::Raw& rawc,
+                        const typename RwWeightsT<Tr>::Raw& rawn) {
+            const int s2 = s + 2 < KT ? s + 2 : KT - 1;
+            const int s3 = s + 3 < KT ? s + 3 : KT - 1;
+            const int a1 = (s + 1) % 3, a2buf = (s + 2) % 3;
+            sub(B[0], sAc, 1, rawn, 0, absrow(a1, 0), pb, ab, pa, aa, B[3]);
+            sub(B[1], sAc, 2, rawn, 1, absrow(a1, 1), pa, aa, pb, ab, B[0]);
+            sub(B[2], sAc, 3, rawn, 2, absrow(a1, 2), pb, ab, pa, aa, B[1]);
+            wait_vmem();
+            store_abs(a2buf, a_next);
+            __syncthreads();  // dY(s + 1), tile and absmax of step s + 2 ready; sAc free
+            RwWeightsT<Tr>::read(cur ? tile1 : tile0, traddr, rawc);  // step s + 2's tile into the freed registers
+            if (copies) as.issue((int64_t)s2 * BK, cur);
+            copy_w(s3, cur ^ 1);  // tile s + 1 left that buffer a barrier ago
+            a_next = load_abs(s3);
+            sub(B[3], sAn, 0, rawn, 3, absrow(a1, 3), pa, aa, pb, ab, B[2]);
+        };
+        int s = 0;
+        for (; s + 1 < KT; s += 2) {
+            step(s, sA0, sA1, 0, raw0, raw1);
+            step(s + 1, sA1, sA0, 1, raw1, raw0);
+        }
+        if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
+        wait_vmem();  // the loads past the last step (clamped to it) land before the epilogue reuses LDS
+    };
+#else
     // The main loop over the first FBA row fragments (as in k_gemm_fwd_rw: an
     // item with at most 64 / 128 valid rows runs 2 / 4 of them, and only the
     // waves whose rows hold them copy dY).
@@ -1591,6 +1793,7 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
         }
         if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
     };
+#endif
     const int64_t valid = grp.rows - m0;  // uniform over the work-group
     if constexpr (STM_SHORT_ITEMS && FB == 8) {
         if (valid <= 64)
@@ -2250,15 +2453,30 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
 
 }  // namespace
 
+// Cost of an expert's rows in units of one 256-row item of the grouped
+// forward. 256-row tiles: one unit per full tile; the last, partial tile runs
+// as a short item when it holds at most 64 or 128 rows (its MFMAs cut to a
+// quarter or half, its weight work and fixed cost not). 192-row tiles: 0.81
+// each (three quarters of the rows, 8 % dearer per row: the weight is
+// dequantized for fewer rows). Measured on the 128-expert bank with 454-569
+// rows per expert: 256-row tiles 462 us (gate/up) and 278 us (down) against
+// 488 and 282 with 192-row tiles.
+double grouped_cost(int64_t r, int bm) {
+    if (r <= 0) return 0.0;
+    if (bm == 192) return 0.81 * (double)((r + 191) / 192);
+    const int64_t rem = r % 256;
+    const double last = rem == 0 ? 0.0 : rem <= 64 ? 0.45 : rem <= 128 ? 0.6 : 1.0;
+    return (double)(r / 256) + last;
+}
+
 int grouped_tile_rows(const int32_t* offsets, int num_experts) {
-    int64_t rows256 = 0, rows192 = 0;
+    double c256 = 0.0, c192 = 0.0;
     for (int e = 0; e < num_experts; ++e) {
         const int64_t r = (int64_t)offsets[e + 1] - offsets[e];
-        if (r <= 0) continue;
-        rows256 += (r + 255) / 256 * 256;
-        rows192 += (r + 191) / 192 * 192;
+        c256 += grouped_cost(r, 256);
+        c192 += grouped_cost(r, 192);
     }
-    return (double)rows192 * 1.08 < (double)rows256 ? 192 : 256;
+    return c192 < c256 ? 192 : 256;
 }
 
 int set_gemm_tile(int kind) {

@@ -324,15 +324,17 @@ def test_noalloc_forward_refuses_oversized_problems_before_touching_a_gpu(L):
 
 @pytest.mark.parametrize("counts, rows", [
     # top-8 of 8192 tokens over 128 experts: ~512 rows each, half just above 512.
-    # 256-row tiles compute 64 * 768 + 64 * 512 = 81920 rows, 192-row tiles
-    # 128 * 576 = 73728 (x 1.08 = 79626): the shorter tile
-    ([540] * 64 + [490] * 64, 192),
-    ([512] * 16, 256),          # 8192 rows either way at 256, 9216 * 1.08 at 192
+    # 256-row tiles: 64 * (2 + 0.45) + 64 * 2 = 284.8 units; 192-row tiles
+    # 128 * 3 * 0.81 = 311: the 256-row tile with a short last item
+    ([540] * 64 + [490] * 64, 256),
+    ([512] * 16, 256),          # 32 units against 38.9
     ([256] * 8, 256),           # exact 256-row tiles
-    ([100] * 8, 192),           # 192 < 256 padded rows, 207 weighted
+    ([100] * 8, 256),           # one 128-row short item each (0.6) against one 192-row item (0.81)
+    ([180, 190] * 4, 192),      # 192-row items (0.81) against full 256-row items (1)
     ([0, 0, 0], 256),           # nothing to compute: the default
-    ([0, 520, 0, 515], 192),    # empty experts skipped: 1536 vs 1152 * 1.08
-    ([700], 256),               # 768 vs 768 * 1.08
+    ([0, 520, 0, 515], 192),    # empty experts skipped: 4.9 units against 4.86
+    ([576] * 4, 192),           # 3 * 0.81 = 2.43 against 2 + 0.45 = 2.45
+    ([700], 256),               # 3 units against 3.24
 ])
 def test_grouped_tile_rows_picks_the_fewest_padded_rows(L, counts, rows):
     import numpy as np

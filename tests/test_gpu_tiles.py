@@ -215,15 +215,15 @@ def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_forward_picks_192_row_tiles_from_host_counts(cuda, monkeypatch, dtype):
-    """32 experts of 540 or 490 rows (one empty, one of 1 row): 256-row tiles
-    would compute 19456 rows, 192-row tiles 17472 (x 1.08 = 18870), so with
-    enough tiles to fill the GPU the library's own choice is the 192-row
-    register-weight kernel (seen in the profile); its result matches the fp32
-    reference per expert and the forced 256-row kernel."""
+    """32 experts of 180 or 190 rows (one empty, one of 1 row): one 192-row
+    item each (0.81 units) against one full 256-row item (1 unit), so the
+    library's own choice is the 192-row register-weight kernel (seen in the
+    profile); its result matches the fp32 reference per expert and the forced
+    256-row kernel."""
     from stratum_amd import _lib
     from stratum_amd.functional import nf4_grouped_gemm
     E, N, K = 32, 1536, 512
-    counts = [540, 490] * 15 + [0, 1]
+    counts = [180, 190] * 15 + [0, 1]
     off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
     assert _lib.lib().stm_nf4_grouped_tile_rows(off.data_ptr(), E) == 192
     w = seeded((E, N, K), 91, 0.02, torch.float16)
