@@ -268,12 +268,33 @@ def run_lora_step(args):
 
     # The headline measures the fused dequant-GEMMs (forced for every row count);
     # the library default for this M (dequantize + hipBLASLt) is reported beside it.
+    # During the timed steps each fused GEMM launch is bracketed by HIP events on
+    # the stream it is launched on: the roofline's kernel duration is the mean
+    # over the timed region itself.
+    import importlib
+    NL = importlib.import_module("stratum_amd.nf4_linear")  # the package also exports a function of that name
+    spans = {"fwd": [], "bwd": []}
+
+    def bracketed(fn, key):
+        def call(*a, **kw):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            out = fn(*a, **kw)
+            end.record()
+            spans[key].append((start, end))
+            return out
+        return call
+
     policy = os.environ.get("STRATUM_NF4_FUSED_MAX_ROWS")
     os.environ["STRATUM_NF4_FUSED_MAX_ROWS"] = "-1"
     try:
         for _ in range(args.warmup):
             step()
-        elapsed = timed_steps(args.steps)
+        NL.nf4_gemm_fwd, NL.nf4_gemm_bwd_dx = bracketed(nf4_gemm_fwd, "fwd"), bracketed(nf4_gemm_bwd_dx, "bwd")
+        try:
+            elapsed = timed_steps(args.steps)
+        finally:
+            NL.nf4_gemm_fwd, NL.nf4_gemm_bwd_dx = nf4_gemm_fwd, nf4_gemm_bwd_dx
     finally:
         if policy is None:
             del os.environ["STRATUM_NF4_FUSED_MAX_ROWS"]
@@ -329,8 +350,9 @@ def run_lora_step(args):
 
     xd = x.detach()
     reps = max(5, args.kernel_reps)
-    fwd_ms = event_time_ms(torch, lambda: nf4_gemm_fwd(xd, packed, absmax, (N, K), 64), reps)
-    bwd_ms = event_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy, packed, absmax, (N, K), 64), reps)
+    assert len(spans["fwd"]) == len(spans["bwd"]) == args.steps, {k: len(v) for k, v in spans.items()}
+    fwd_ms = sum(a.elapsed_time(b) for a, b in spans["fwd"]) / args.steps
+    bwd_ms = sum(a.elapsed_time(b) for a, b in spans["bwd"]) / args.steps
     gemm_flops = 2.0 * M * N * K
     fwd_tf = gemm_flops / (fwd_ms * 1e-3) / 1e12
     bwd_tf = gemm_flops / (bwd_ms * 1e-3) / 1e12
@@ -390,7 +412,8 @@ def run_lora_step(args):
                      "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic.get("k_gemm_fwd_rw"),
                      "traffic_source": "profiles/traffic_lora_step_w14336x4096_x8192.json (rocprofv3 "
                                        "FETCH_SIZE + WRITE_SIZE per launch, calibrated; not measured in this run)",
-                     "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops},
+                     "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops,
+                     "timing": "HIP events around each launch on its stream, mean over the timed steps"},
         "bwd_dx": {"kernel": "k_gemm_bwd_rw<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
         "dequant": {"kernel": "k_dequantize<BF16>", "value": round(deq_gbs, 1), "unit": "GB/s",
