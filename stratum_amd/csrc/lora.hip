@@ -50,6 +50,7 @@ constexpr int LR_QS = LR_SM + 8;   // bf16 stride of a staged Q rank row (144 by
 __device__ __forceinline__ int zswz(int m) { return (m & 15) ^ (((m >> 3) & 3) << 1); }
 
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 template <typename Tr>
@@ -176,6 +177,7 @@ __global__ __launch_bounds__(256, 2) void k_lora_pass(LoraArgs g) {
         }
     };
 
+    const __attribute__((address_space(3))) uint4* lds_zt = (const __attribute__((address_space(3))) uint4*)zt;
     f32x4_t acc_col[4][G];
 #pragma unroll
     for (int f = 0; f < 4; ++f)
@@ -218,14 +220,22 @@ __global__ __launch_bounds__(256, 2) void k_lora_pass(LoraArgs g) {
                     a[k] = *reinterpret_cast<const uint4*>(qs + (16 * k + lr) * LR_QS + 32 * mc + 8 * lh);
 #pragma unroll 1
                 for (int f = 0; f < 4; ++f) {
-                    const int c = 64 * wave + 16 * f + lr, q = c >> 3, e = c & 7;
-                    s16x8_t v;
+                    // lane lr needs rows 32 mc + 8 lh + 0..7 of column 64 w + 16 f + lr:
+                    // two transposed reads of 4 rows x 16 columns, in which lane s of
+                    // the 16-lane group points at 4 columns 4 (s % 4) .. of row s / 4
+                    // and receives column s of the 4 rows (gfx950 lane layout)
+                    const int tc = 64 * wave + 16 * f + 4 * (lr & 3);
+                    uint2 half[2];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int m = 32 * mc + 8 * lh + i;
-                        v[i] = reinterpret_cast<const short*>(zt)[(m * LR_CH + (q ^ zswz(m))) * 8 + e];
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int m = 32 * mc + 8 * lh + 4 * hh + (lr >> 2);
+                        const uint32_t byte = (uint32_t)((m * LR_CH + ((tc >> 3) ^ zswz(m))) * 16 + (tc & 7) * 2);
+                        const s16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) s16x4_t*)((__attribute__((address_space(3))) char*)
+                                                                             lds_zt + byte));
+                        half[hh] = __builtin_bit_cast(uint2, t);
                     }
-                    const uint4 b = __builtin_bit_cast(uint4, v);
+                    const uint4 b = make_uint4(half[0].x, half[0].y, half[1].x, half[1].y);
 #pragma unroll
                     for (int k = 0; k < G; ++k) acc_col[f][k] = mfma16x32<Tr>(a[k], b, acc_col[f][k]);
                 }
