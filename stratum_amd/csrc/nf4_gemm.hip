@@ -260,21 +260,21 @@ __device__ __forceinline__ float level_from_immediates(int i) {
 }
 
 // Entries (level[b >> 4], level[b & 15]) at index copies * b + c, written by NT
-// threads: lane l holds level l % 16 and each entry gathers its two levels
-// across lanes, so filling costs no memory round trips (a load per entry
-// would put a dozen dependent round trips at the start of every block).
+// threads. Pair p = (lo, c) = (p / copies, p % copies) belongs to thread
+// p % NT; it writes the 16 entries b = 16 hi + lo, hi = 0..15, whose first
+// level is an immediate and whose second is the thread's one selected level:
+// 16 independent LDS writes, no memory or cross-lane round trips.
 template <int NT, int COPIES>
 __device__ __forceinline__ void fill_level_table(float2* lut, int tid) {
-    constexpr int ENTRIES = 256 * COPIES, ITERS = (ENTRIES + NT - 1) / NT;
-    const int mine = __float_as_int(level_from_immediates(tid & 15));
+    constexpr int PAIRS = 16 * COPIES, ITERS = (PAIRS + NT - 1) / NT;
 #pragma unroll
     for (int i = 0; i < ITERS; ++i) {
-        // every lane takes part in the gathers; a last partial pass (NT not
-        // dividing the table) only skips the write
-        const int t = tid + NT * i, b = (t < ENTRIES ? t : ENTRIES - 1) / COPIES;
-        const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((b >> 4) << 2, mine));
-        const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((b & 15) << 2, mine));
-        if (ENTRIES % NT == 0 || t < ENTRIES) lut[t] = make_float2(hi, lo);
+        const int p = tid + NT * i;
+        if (PAIRS % NT != 0 && p >= PAIRS) break;
+        const int lo = p / COPIES, c = p % COPIES;
+        const float lv = level_from_immediates(lo);
+#pragma unroll
+        for (int hi = 0; hi < 16; ++hi) lut[(16 * hi + lo) * COPIES + c] = make_float2(kLevelsDev[hi], lv);
     }
 }
 
