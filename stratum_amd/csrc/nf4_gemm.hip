@@ -184,6 +184,109 @@ __device__ __forceinline__ int64_t item_order(int64_t w, int64_t work, int num_g
     return w < W8 ? (w % 8) * (work / 8) + w / 8 : w;
 }
 
+// 1: grouped launches of the register-weight kernels walk a compact item list
+// (GroupedPlan); 0: every expert gets ceil(max_rows / BM) row-tile slots.
+#ifndef STM_GROUPED_PLAN
+#define STM_GROUPED_PLAN 1
+#endif
+
+// Compact item list of a grouped launch, built by every work-group from the
+// device offsets at kernel start. Expert e holds nt_e = ceil(rows_e / BM) row
+// tiles. Its last tile is a tail when it holds at most 128 rows (a short item:
+// a quarter or half of the MFMAs, the full weight work); every other tile is a
+// main tile. Items run all main tiles first (experts in order, an expert's
+// tiles column-tile-major, as the slot order had them), then all tails, each
+// class in contiguous per-XCD runs. So every work-group gets the same number
+// of main items (up to one), the cheap tails even out the rest, and slots past
+// an expert's rows are never enumerated. Thread t owns experts 2t and 2t + 1.
+constexpr int kPlanExperts = 512;
+struct GroupedPlan {
+    int off[kPlanExperts + 1];       // the expert offsets
+    int pre_main[kPlanExperts + 1];  // exclusive prefix of main tiles over experts
+    int pre_tail[kPlanExperts + 1];  // exclusive prefix of tails (0 or 1 per expert)
+};
+
+__device__ __forceinline__ bool plan_usable(const GemmArgs& g) {
+    return STM_GROUPED_PLAN && g.num_groups > 1 && g.offsets && g.num_groups <= kPlanExperts && g.splits == 1;
+}
+
+// Ends with a barrier: the plan is visible to every wave.
+template <int BM>
+__device__ void build_plan(const GemmArgs& g, GroupedPlan& P, int tid) {
+    static_assert(2 * 256 == kPlanExperts, "256 threads, two experts each");
+    __shared__ int wave_tot[2][4];
+    const int E = g.num_groups, lane = tid & 63, wave = tid >> 6;
+    int m[2], t[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int e = 2 * tid + i;
+        m[i] = t[i] = 0;
+        if (e < E) {
+            const int r0 = g.offsets[e], r1 = g.offsets[e + 1];
+            P.off[e] = r0;
+            if (e == E - 1) P.off[E] = r1;
+            const int rows = r1 - r0;
+            const int nt = (rows + BM - 1) / BM;
+            t[i] = nt > 0 && rows - (nt - 1) * BM <= 128 ? 1 : 0;
+            m[i] = nt - t[i];
+        }
+    }
+    int sm = m[0] + m[1], st = t[0] + t[1];  // inclusive scans over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int om = __shfl_up(sm, d), ot = __shfl_up(st, d);
+        if (lane >= d) sm += om, st += ot;
+    }
+    if (lane == 63) wave_tot[0][wave] = sm, wave_tot[1][wave] = st;
+    __syncthreads();
+    for (int v = 0; v < wave; ++v) sm += wave_tot[0][v], st += wave_tot[1][v];
+    const int em = sm - m[0] - m[1], et = st - t[0] - t[1];  // exclusive
+    P.pre_main[2 * tid] = em;
+    P.pre_main[2 * tid + 1] = em + m[0];
+    P.pre_tail[2 * tid] = et;
+    P.pre_tail[2 * tid + 1] = et + t[0];
+    if (tid == 255) P.pre_main[kPlanExperts] = sm, P.pre_tail[kPlanExperts] = st;
+    __syncthreads();
+}
+
+// Item w of the plan's list: expert e, row tile tm, column tile tn (ntn column
+// tiles). Every lane of the wave takes part (the expert search is a ballot).
+template <int BM>
+__device__ __forceinline__ void plan_item(const GroupedPlan& P, int E, int64_t ntn, int64_t w, int64_t main_work,
+                                          int64_t work, int lane, int& e, int64_t& tm, int64_t& tn) {
+    const bool is_main = w < main_work;
+    int64_t u = is_main ? w : w - main_work;
+    u = item_order(u, is_main ? main_work : work - main_work, 2);
+    const int* pre = is_main ? P.pre_main : P.pre_tail;
+    // the expert: one less than the number of experts whose first item is at or before u
+    int cnt = 0;
+    for (int j = 0; 64 * j < E; ++j) {
+        const int ee = 64 * j + lane;
+        cnt += __popcll(__ballot(ee < E && (int64_t)pre[ee] * ntn <= u));
+    }
+    e = __builtin_amdgcn_readfirstlane(cnt - 1);
+    const int64_t local = u - (int64_t)pre[e] * ntn;
+    if (is_main) {
+        const int64_t n_e = pre[e + 1] - pre[e];
+        tn = local / n_e;
+        tm = local % n_e;
+    } else {
+        const int rows = P.off[e + 1] - P.off[e];
+        tm = (rows + BM - 1) / BM - 1;
+        tn = local;
+    }
+}
+
+__device__ __forceinline__ Group plan_group(const GemmArgs& g, const GroupedPlan& P, int e) {
+    Group r;
+    r.row0 = P.off[e];
+    r.rows = (int64_t)P.off[e + 1] - r.row0;
+    const int64_t wnum = g.N * g.K;
+    r.packed = g.packed + (int64_t)e * (wnum / 2);
+    r.absmax = g.absmax + (int64_t)e * (wnum / g.blocksize);
+    return r;
+}
+
 // Activation staging: the tile rows [m0, m0 + BM) x [k0, k0 + 64) are copied
 // into an LDS buffer (BM x 8 chunks) with XI direct copies per wave per step.
 // Per-lane global row pointers and the wave-uniform LDS bases of both buffers
@@ -936,14 +1039,32 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
 
     const int64_t K = g.K, N = g.N;
     const int64_t ntm = (g.M + BM - 1) / BM, ntn = (N + BN - 1) / BN, tiles = ntm * ntn;
-    const int64_t work = tiles * g.num_groups * g.splits;
+    int64_t work = tiles * g.num_groups * g.splits, main_work = 0;
+    __shared__ GroupedPlan plan;
+    bool use_plan = false;
+    if constexpr (NT == 256) {
+        use_plan = plan_usable(g);
+        if (use_plan) {
+            build_plan<BM>(g, plan, tid);
+            main_work = (int64_t)plan.pre_main[kPlanExperts] * ntn;
+            work = main_work + (int64_t)plan.pre_tail[kPlanExperts] * ntn;
+        }
+    }
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // work items (tile, expert, split) as in k_gemm_fwd
-    const int64_t wi = item_order(w, work, g.num_groups);
-    const int64_t rest = wi / tiles;
-    const int z = (int)(rest / g.num_groups);
-    const Group grp = group_of(g, (int)(rest % g.num_groups));
+    int z = 0;
+    Group grp;
     int64_t tm, tn;
-    tile_coords(wi % tiles, ntm, ntn, tm, tn, g.num_groups == 1);
+    if (use_plan) {
+        int e;
+        plan_item<BM>(plan, g.num_groups, ntn, w, main_work, work, lane0, e, tm, tn);
+        grp = plan_group(g, plan, e);
+    } else {
+        const int64_t wi = item_order(w, work, g.num_groups);
+        const int64_t rest = wi / tiles;
+        z = (int)(rest / g.num_groups);
+        grp = group_of(g, (int)(rest % g.num_groups));
+        tile_coords(wi % tiles, ntm, ntn, tm, tn, g.num_groups == 1);
+    }
     const int64_t m0 = tm * BM, n0 = tn * BN;
     if (m0 >= grp.rows) continue;
 
@@ -1538,14 +1659,29 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 
     const int64_t K = g.K, N = g.N;
     const int64_t ntm = (g.M + BM - 1) / BM, ntk = (K + BN - 1) / BN, tiles = ntm * ntk;
-    const int64_t work = tiles * g.num_groups * g.splits;
+    int64_t work = tiles * g.num_groups * g.splits, main_work = 0;
+    __shared__ GroupedPlan plan;
+    const bool use_plan = plan_usable(g);
+    if (use_plan) {
+        build_plan<BM>(g, plan, tid);
+        main_work = (int64_t)plan.pre_main[kPlanExperts] * ntk;
+        work = main_work + (int64_t)plan.pre_tail[kPlanExperts] * ntk;
+    }
     for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {  // items (tile, expert, split)
-    const int64_t wi = item_order(w, work, g.num_groups);
-    const int64_t rest = wi / tiles;
-    const int z = (int)(rest / g.num_groups);
-    const Group grp = group_of(g, (int)(rest % g.num_groups));
+    int z = 0;
+    Group grp;
     int64_t tm, tk;
-    tile_coords(wi % tiles, ntm, ntk, tm, tk, g.num_groups == 1);
+    if (use_plan) {
+        int e;
+        plan_item<BM>(plan, g.num_groups, ntk, w, main_work, work, lane0, e, tm, tk);
+        grp = plan_group(g, plan, e);
+    } else {
+        const int64_t wi = item_order(w, work, g.num_groups);
+        const int64_t rest = wi / tiles;
+        z = (int)(rest / g.num_groups);
+        grp = group_of(g, (int)(rest % g.num_groups));
+        tile_coords(wi % tiles, ntm, ntk, tm, tk, g.num_groups == 1);
+    }
     const int64_t m0 = tm * BM, k0 = tk * BN;
     if (m0 >= grp.rows) continue;
 
