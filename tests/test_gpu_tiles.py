@@ -213,6 +213,43 @@ def test_grouped_every_tile(cuda, monkeypatch, dtype, tile):
         assert rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype], e
 
 
+@pytest.mark.parametrize("tile", [None, "big"])
+@pytest.mark.parametrize("E", [512, 513])
+def test_grouped_item_list_at_the_expert_limit(cuda, monkeypatch, E, tile):
+    """The register-weight kernels build their grouped item list in LDS for up
+    to 512 experts and enumerate max_rows slots per expert above that. Both
+    sides of the limit, with empty and 1-row experts, last tiles of exactly 64,
+    65, 128, 129 and 256 rows (tail / main boundaries) and multi-tile experts:
+    forward and input gradient per expert against the oracle weights."""
+    from stratum_amd.functional import nf4_grouped_gemm
+    set_tile(monkeypatch, tile)
+    N, K = 256, 128
+    dtype = torch.bfloat16
+    rng = np.random.default_rng(E)
+    counts = rng.integers(0, 200, E)
+    special = [0, 1, 64, 65, 128, 129, 256, 257, 256 + 64, 256 + 65, 256 + 128, 256 + 129, 600]
+    counts[:len(special)] = special
+    counts[-1] = 0
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    Mt = int(off[-1])
+    w = seeded((E, N, K), 93, 0.02, torch.float16)
+    bits = w.reshape(-1, K).contiguous().view(torch.int16).numpy().view(np.uint16)
+    rp, ra = C.quantize(bits, O.DT_F16, 64, "argmin")
+    deq = C.dequantize(rp, ra, E * N * K, 64, TAG[dtype]).view(np.int16).reshape(E, N, K)
+    wq = torch.from_numpy(deq).view(dtype).float().to(cuda)
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    x = seeded((Mt, K), 94, 1.0, dtype).to(cuda)
+    dy = seeded((Mt, N), 95, 1.0, dtype).to(cuda)
+    y = nf4_grouped_gemm(x, q, a, off, (N, K), 64)
+    dx = nf4_grouped_gemm(dy, q, a, off, (N, K), 64, backward=True)
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], (e, hi - lo)
+        assert rel(dx[lo:hi], dy[lo:hi].float() @ wq[e]) <= TOL[dtype], (e, hi - lo)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_forward_picks_192_row_tiles_from_host_counts(cuda, monkeypatch, dtype):
     """32 experts of 180 or 190 rows (one empty, one of 1 row): one 192-row
