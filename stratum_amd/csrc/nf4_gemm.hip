@@ -1012,14 +1012,6 @@ __device__ __forceinline__ void rw_slot_pattern() {
     }
 }
 
-// 1: the forward register-weight kernel issues each step's loads right after
-// the barrier that frees their destination (a whole step to land); 0: the
-// activation copy at the start of the step and the weight loads after its
-// first sub-step.
-#ifndef STM_RW_EARLY_LOADS
-#define STM_RW_EARLY_LOADS 1
-#endif
-
 // Items with at most 64 / 128 valid rows run the 256-row register-weight
 // kernels' main loop over 2 / 4 of the 8 row fragments (1: on).
 #ifndef STM_SHORT_ITEMS
@@ -1109,7 +1101,6 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
     // (64 or 128 rows): a quarter or half of the MFMAs, the same weight work,
     // and only the waves whose rows hold them copy activations. Rows past the
     // valid ones are never stored.
-#if STM_RW_EARLY_LOADS
     // The activation tile of step s + 2 and the packed words of step s + 3 are
     // issued right after the barrier that frees their destination (the buffer
     // step s has just released; the words of step s + 1, whose last table reads
@@ -1181,64 +1172,6 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
         if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
         wait_vmem();  // the loads past the last step (clamped to it) land before the epilogue reuses LDS
     };
-#else
-    auto main_loop = [&](auto fba_tag) {
-        constexpr int FBA = decltype(fba_tag)::value;
-        // wave w copies the activation rows [w R, w R + R), R = BM / (4 WM)
-        const bool copies = FBA == FB || wave * (BM / (4 * WM)) < 32 * FBA;
-
-        // prologue: activation tile 0, packed weights of steps 0 and 1, fragments
-        // of sub-steps 0..2 of step 0, table reads of its sub-step 3
-        ws.load(0, raw0);
-        ws.load(KT > 1 ? BK : 0, raw1);
-        if (copies) as.issue(0, 0);
-        wait_vmem();
-        __syncthreads();  // level table and activation tile 0 ready
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            ws.issue(raw0, j, pa);
-            RwWeights<Tr>::finish(raw0, pa, B[j]);
-        }
-        ws.issue(raw0, 3, pa);
-        read_x<FB, FBA>(x, sA0, xrow0, lane, 0);
-        sched_fence();
-
-        // one sub-step: MFMAs on (w, x) reloading x with sub-step jn from sx, table
-        // reads into p_next, fragments from p_cur (absmax of r_cur) into bout; the
-        // scheduler interleaves them as 2 VALU, 1 LDS read, 1 MFMA per slot
-        auto sub = [&](const uint4 (&w)[2], const uint4* sx, int jn, const typename RwWeights<Tr>::Raw& r_next,
-                       int word_next, f32x2_t (&p_next)[2][4], const typename RwWeights<Tr>::Raw& r_cur,
-                       const f32x2_t (&p_cur)[2][4], uint4 (&bout)[2]) {
-            ws.issue(r_next, word_next, p_next);
-            mma_sub<Tr, 2, FB, FBA>(acc, w, x, sx, xrow0, lane, jn);
-            RwWeights<Tr>::finish(r_cur, p_cur, bout);
-            rw_slot_pattern<2 * FBA>();
-            sched_fence();
-        };
-
-        // step s: rawc holds step s's packed weights (refilled with step s + 2 once
-        // its absmax has been used), rawn step s + 1's
-        auto step = [&](int s, const uint4* sAc, const uint4* sAn, int nbuf, typename RwWeights<Tr>::Raw& rawc,
-                        const typename RwWeights<Tr>::Raw& rawn) {
-            const int s1 = s + 1 < KT ? s + 1 : KT - 1;
-            const int s2 = s + 2 < KT ? s + 2 : KT - 1;
-            if (copies) as.issue((int64_t)s1 * BK, nbuf);
-            sub(B[0], sAc, 1, rawn, 0, pb, rawc, pa, B[3]);
-            ws.load((int64_t)s2 * BK, rawc);
-            sub(B[1], sAc, 2, rawn, 1, pa, rawn, pb, B[0]);
-            sub(B[2], sAc, 3, rawn, 2, pb, rawn, pa, B[1]);
-            wait_vmem();
-            __syncthreads();  // activation tile s + 1 in sAn; every wave is done reading sAc
-            sub(B[3], sAn, 0, rawn, 3, pa, rawn, pb, B[2]);
-        };
-        int s = 0;
-        for (; s + 1 < KT; s += 2) {
-            step(s, sA0, sA1, 1, raw0, raw1);
-            step(s + 1, sA1, sA0, 0, raw1, raw0);
-        }
-        if (s < KT) step(s, sA0, sA1, 1, raw0, raw1);
-    };
-#endif
     // the item's valid rows decide (uniform over the work-group, so every wave
     // takes the same branch and meets the same barriers)
     const int64_t valid = grp.rows - m0;
@@ -1759,7 +1692,6 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
     const int xh = lane >> 5;
     auto xch = [&](int j) { return 4 * (j >> 1) + 2 * xh + (j & 1); };
 
-#if STM_RW_EARLY_LOADS
     // The main loop over the first FBA row fragments (as in k_gemm_fwd_rw: an
     // item with at most 64 / 128 valid rows runs 2 / 4 of them, and only the
     // waves whose rows hold them copy dY). Each step's loads are issued right
@@ -1851,85 +1783,6 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
         if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
         wait_vmem();  // the loads past the last step (clamped to it) land before the epilogue reuses LDS
     };
-#else
-    // The main loop over the first FBA row fragments (as in k_gemm_fwd_rw: an
-    // item with at most 64 / 128 valid rows runs 2 / 4 of them, and only the
-    // waves whose rows hold them copy dY).
-    auto main_loop = [&](auto fba_tag) {
-        constexpr int FBA = decltype(fba_tag)::value;
-        // wave w copies the dY rows [w BM / 4, (w + 1) BM / 4)
-        const bool copies = FBA == FB || wave * (BM / 4) < 32 * FBA;
-
-        // prologue: dY(0), packed tiles of steps 0 and 1, absmax of steps 0 and 1;
-        // fragments of sub-steps 0..2 of step 0, table reads of its sub-step 3
-        {
-            const float a0 = load_abs(0), a1 = load_abs(KT > 1 ? 1 : 0);
-            if (copies) as.issue(0, 0);
-            copy_w(0, 0);
-            copy_w(KT > 1 ? 1 : 0, 1);
-            wait_vmem();
-            store_abs(0, a0);
-            store_abs(1, a1);  // absmax of step s in buffer s % 3
-        }
-        __syncthreads();  // level table, dY(0), tiles 0 and 1, absmax 0 and 1 ready
-        RwWeightsT<Tr>::read(tile0, traddr, raw0);
-        RwWeightsT<Tr>::read(tile1, traddr, raw1);
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            ws.issue(raw0, j, pa, absrow(0, j), aa);
-            RwWeightsT<Tr>::finish(pa, aa, B[j]);
-        }
-        ws.issue(raw0, 3, pa, absrow(0, 3), aa);
-        // activation fragments of sub-step 0
-#pragma unroll
-        for (int f = 0; f < FBA; ++f) x[f] = sA0[swz(f * 32 + (lane & 31), xch(0))];
-        __syncthreads();  // every wave has read tile 0 before step 0 copies into its buffer
-
-        auto sub = [&](const uint4 (&wf)[2], const uint4* sx, int jn, const typename RwWeightsT<Tr>::Raw& r_next,
-                       int j_next, uint32_t arow_next, f32x2_t (&p_next)[2][4], f32x4_t (&a_next)[2],
-                       const f32x2_t (&p_cur)[2][4], const f32x4_t (&a_cur)[2], uint4 (&bout)[2]) {
-            ws.issue(r_next, j_next, p_next, arow_next, a_next);
-            const int ch = xch(jn);
-#pragma unroll
-            for (int f = 0; f < FBA; ++f) {
-                acc[0][f] = mfma<Tr>(wf[0], x[f], acc[0][f]);
-                acc[1][f] = mfma<Tr>(wf[1], x[f], acc[1][f]);
-                x[f] = sx[swz(f * 32 + (lane & 31), ch)];
-            }
-            RwWeightsT<Tr>::finish(p_cur, a_cur, bout);
-            rw_slot_pattern<2 * FBA>();
-            sched_fence();
-        };
-
-        // step s: rawc = transposed tile of step s (its sub-step 3 not yet made),
-        // rawn = step s + 1; dY(s) in sAc; tiles alternate (step s in buffer cur),
-        // absmax buffers rotate over three (step s + 1 in a1, step s + 2 into a2buf,
-        // whose last reader, step s - 2's sub-step 3, is a barrier behind)
-        auto step = [&](int s, const uint4* sAc, const uint4* sAn, int cur, typename RwWeightsT<Tr>::Raw& rawc,
-                        const typename RwWeightsT<Tr>::Raw& rawn) {
-            const int s1 = s + 1 < KT ? s + 1 : KT - 1;
-            const int s2 = s + 2 < KT ? s + 2 : KT - 1;
-            const int a1 = (s + 1) % 3, a2buf = (s + 2) % 3;
-            const float a2 = load_abs(s2);
-            if (copies) as.issue((int64_t)s1 * BK, cur ^ 1);
-            copy_w(s2, cur);  // the tile of step s was read transposed one barrier ago
-            sub(B[0], sAc, 1, rawn, 0, absrow(a1, 0), pb, ab, pa, aa, B[3]);
-            sub(B[1], sAc, 2, rawn, 1, absrow(a1, 1), pa, aa, pb, ab, B[0]);
-            sub(B[2], sAc, 3, rawn, 2, absrow(a1, 2), pb, ab, pa, aa, B[1]);
-            wait_vmem();
-            store_abs(a2buf, a2);
-            __syncthreads();  // dY(s + 1), tile and absmax of step s + 2 ready; sAc free
-            RwWeightsT<Tr>::read(cur ? tile1 : tile0, traddr, rawc);  // step s + 2's tile into the freed registers
-            sub(B[3], sAn, 0, rawn, 3, absrow(a1, 3), pa, aa, pb, ab, B[2]);
-        };
-        int s = 0;
-        for (; s + 1 < KT; s += 2) {
-            step(s, sA0, sA1, 0, raw0, raw1);
-            step(s + 1, sA1, sA0, 1, raw1, raw0);
-        }
-        if (s < KT) step(s, sA0, sA1, 0, raw0, raw1);
-    };
-#endif
     const int64_t valid = grp.rows - m0;  // uniform over the work-group
     if constexpr (STM_SHORT_ITEMS && FB == 8) {
         if (valid <= 64)
