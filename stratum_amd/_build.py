@@ -32,6 +32,13 @@ FLAGS = [
     "-Wno-unused-function",
 ]
 
+# Per-source additions. The GEMM kernels are scheduled with LLVM's iterative
+# ILP strategy: 1-3 % faster on most fused GEMM shapes (A/B-timed against the
+# default scheduler, outputs bit-identical).
+SOURCE_FLAGS = {
+    "nf4_gemm.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
 
 def _run(cmd: list, verbose: bool) -> subprocess.Popen:
     if verbose:
@@ -62,7 +69,9 @@ def build(verbose: bool = False) -> str:
         for src in SOURCES:
             obj = os.path.join(tmpdir, os.path.splitext(src)[0] + ".o")
             objs.append(obj)
-            procs.append((_run([HIPCC, *compile_flags, "-c", os.path.join(CSRC, src), "-o", obj], verbose), src))
+            extra = SOURCE_FLAGS.get(src, [])
+            procs.append((_run([HIPCC, *compile_flags, *extra, "-c", os.path.join(CSRC, src), "-o", obj], verbose),
+                          src))
         for proc, src in procs:
             _finish(proc, src, verbose)
         tmp = LIB_PATH + ".tmp"
