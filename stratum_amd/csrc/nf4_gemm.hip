@@ -2048,6 +2048,261 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
         }
 }
 
+// Small-M forward without a split reduction (up to 16 activation rows). A
+// work-group owns 16 T weight rows (T MFMA tiles of 16 rows); a wave takes TW
+// of them (TW = 1 or 2) and the 8 waves split the reduction into S = 8 TW / T
+// slices: wave w takes tiles TW (w % (T / TW)) .. + TW - 1 and slice
+// s = w / (T / TW), and in step j works on group j S + s (256 deep), so one
+// step streams S consecutive groups (S x 128 contiguous bytes of every weight
+// row). Operands reach LDS through lane-contiguous global -> LDS copies,
+// double-buffered, one barrier per step; only the valid activation rows are
+// copied (XR rows per slice; lanes past M use zero activations). The
+// dequantization and MFMAs per group are those of k_gemv_fwd. At the end the
+// slices' sums meet in LDS and the waves of slice 0 add them in slice order,
+// then the rank-R LoRA term and the bias, and store: one launch, no fp32
+// partials.
+template <int T, int TW, int XR>
+struct GkCfg {
+    static constexpr int P = T / TW, S = 8 / P, ROWS = 16 * T;
+    static constexpr int kLut = 256 * RW_LUT_COPIES * 8;
+    static constexpr int kW = S * ROWS * 128;    // packed bytes of the step's S groups
+    static constexpr int kA = S * ROWS * 4 * 4;  // absmax, up to 4 blocks per row and group
+    static constexpr int kX = S * XR * 512;      // activations, XR rows per group
+    static constexpr int kBuf = kW + kA + kX;
+    static constexpr int kLds = kLut + 2 * kBuf;
+    static_assert(T % TW == 0 && 8 % P == 0 && kLds <= 160 * 1024, "LDS");
+    static_assert(S * XR * 32 <= 1024, "at most two activation copies per thread");
+    static_assert(8 * TW * 64 * 16 <= kW, "the slice sums fit the weight buffer");
+};
+
+template <typename Tr, int T, int TW, int XR>
+__global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
+    using C = GkCfg<T, TW, XR>;
+    constexpr int S = C::S, ROWS = C::ROWS, P = C::P;
+    constexpr int RS = S * ROWS;  // row-slices per step: 128 TW
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = (wave % P) * TW, s = wave / P;
+    __shared__ __align__(16) uint8_t smem[C::kLds];
+    float2* lut_all = reinterpret_cast<float2*>(smem);
+    auto bw = [&](int b) { return reinterpret_cast<uint4*>(smem + C::kLut + b * C::kBuf); };  // [S][ROWS][8]
+    auto ba = [&](int b) { return reinterpret_cast<float*>(smem + C::kLut + b * C::kBuf + C::kW); };
+    auto bx = [&](int b) { return reinterpret_cast<uint4*>(smem + C::kLut + b * C::kBuf + C::kW + C::kA); };
+
+    const int64_t K = g.K, N = g.N, M = g.M;
+    const int bshift = 31 - __builtin_clz(g.blocksize);
+    const int nfl = (GV_GK >> bshift) > 0 ? (GV_GK >> bshift) : 1;  // absmax per row per group
+    const int64_t kblocks = K >> bshift;
+    const int ngroups = (int)((K + GV_GK - 1) / GV_GK);
+    const int steps = (ngroups + S - 1) / S;
+    const int64_t n0 = (int64_t)blockIdx.x * ROWS;
+    auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
+
+    // copy sources, per thread. Packed weight: row-slice q = 16 TW wave + 8 i +
+    // lane / 8 of the step's RS, 16-byte piece (lane % 8) ^ key(row).
+    const uint8_t* wsrc[2 * TW];
+    int wsl[2 * TW], wpiece[2 * TW];
+#pragma unroll
+    for (int i = 0; i < 2 * TW; ++i) {
+        const int q = 16 * TW * wave + 8 * i + (lane >> 3), row = q % ROWS;
+        wsl[i] = q / ROWS;
+        wpiece[i] = (lane & 7) ^ ((row >> 1) & 7);
+        const int64_t n = n0 + row < N ? n0 + row : N - 1;
+        wsrc[i] = g.packed + n * (K / 2) + 16 * wpiece[i];
+    }
+    // absmax: thread tid copies entries e = tid + 512 i = (row-slice q) nfl + j
+    // of RS nfl (whole waves: 128 TW nfl entries)
+    const int acount = RS * nfl;
+    const float* asrc[TW];
+    int asl[TW], aj[TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+        const int e = tid + 512 * i, q = (e < acount ? e : 0) / nfl;
+        asl[i] = q / ROWS;
+        aj[i] = e % nfl;
+        const int64_t n = n0 + q % ROWS < N ? n0 + q % ROWS : N - 1;
+        asrc[i] = g.absmax + n * kblocks;
+    }
+    // activations: piece p = tid + 512 i of S x XR x 32 (row xr of slice xs)
+    const uint16_t* xsrc[2];
+    int xsl[2], xpiece[2];
+    bool xon[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = tid + 512 * i, xr = (p / 32) % XR;
+        xsl[i] = p / (XR * 32);
+        xon[i] = p < S * XR * 32 && xr < M;
+        xpiece[i] = (p % 32) ^ (xr & 15);
+        xsrc[i] = reinterpret_cast<const uint16_t*>(g.a) + (xr < M ? xr : 0) * K;
+    }
+
+    auto copy_step = [&](int j, int b) {
+#pragma unroll
+        for (int i = 0; i < 2 * TW; ++i) {
+            int grp = j * S + wsl[i];
+            grp = grp < ngroups ? grp : ngroups - 1;
+            const int64_t off = (int64_t)grp * (GV_GK / 2);
+            // bytes past the row (K % 256 != 0) read the row start instead
+            const uint8_t* src = off + 16 * wpiece[i] < K / 2 ? wsrc[i] + off : wsrc[i] - 16 * wpiece[i];
+            dma16(src, uniform(lds_offset(bw(b) + (16 * TW * wave + 8 * i) * 8)));
+        }
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+            if (tid + 512 * i < acount) {
+                int grp = j * S + asl[i];
+                grp = grp < ngroups ? grp : ngroups - 1;
+                int64_t blk = (((int64_t)grp * GV_GK) >> bshift) + aj[i];
+                blk = blk < kblocks ? blk : kblocks - 1;
+                dma4(asrc[i] + blk, uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(
+                                        ba(b) + 512 * i + 64 * wave))));
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (xon[i]) {
+                int grp = j * S + xsl[i];
+                grp = grp < ngroups ? grp : ngroups - 1;
+                const int64_t k = (int64_t)grp * GV_GK + 8 * xpiece[i];
+                dma16(xsrc[i] + (k < K ? k : 0), uniform(lds_offset(bx(b) + 512 * i + 64 * wave)));
+            }
+    };
+
+    const int r = lane & 15, h = lane >> 4;
+    const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
+    f32x4_t acc[TW];
+#pragma unroll
+    for (int u = 0; u < TW; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int rx = r < XR ? r : 0;
+
+    auto issue = [&](const uint4& qv, f32x2_t (&pp)[4][4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t word = q == 0 ? qv.x : q == 1 ? qv.y : q == 2 ? qv.z : qv.w;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t addr = __builtin_amdgcn_perm(copy_off, word, 0x0C0C0004u | ((uint32_t)b << 8));
+                pp[q][b] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)addr;
+            }
+        }
+    };
+    // group j S + s of buffer b: items i = TW c + u (chunk c of tile t0 + u; k =
+    // 128 c + 32 h + 0..31 on lane (r, h)); the table reads of item i + 1 go out
+    // before item i's math
+    auto compute = [&](int j, int b) {
+        const int grp = j * S + s;
+        if (grp >= ngroups) return;
+        const int64_t kg = (int64_t)grp * GV_GK;
+        uint4 qv[2 * TW], xv[2][4];
+        float av[2 * TW];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const bool ok = kg + 128 * c + 32 * h < K;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = bx(b)[(s * XR + rx) * 32 + ((16 * c + 4 * h + q) ^ r)];
+                xv[c][q] = (ok && r < M) ? v : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < TW; ++u) {
+                const int row = 16 * (t0 + u) + r, qrow = s * ROWS + row;
+                qv[TW * c + u] = bw(b)[qrow * 8 + ((4 * c + h) ^ ((row >> 1) & 7))];
+                const float a = ba(b)[qrow * nfl + ((128 * c + 32 * h) >> bshift)];
+                av[TW * c + u] = ok ? a : 0.0f;
+            }
+        }
+        f32x2_t p[2][4][4];
+        issue(qv[0], p[0]);
+#pragma unroll
+        for (int i = 0; i < 2 * TW; ++i) {
+            if (i + 1 < 2 * TW) issue(qv[i + 1], p[(i + 1) & 1]);
+            sched_fence();
+            const int c = i / TW, u = i % TW;
+            const float a = av[i];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x2_t(&pq)[4] = p[i & 1][q];
+                uint4 w;
+                w.x = Tr::pack2(opaque(pq[0].x * a), opaque(pq[0].y * a));
+                w.y = Tr::pack2(opaque(pq[1].x * a), opaque(pq[1].y * a));
+                w.z = Tr::pack2(opaque(pq[2].x * a), opaque(pq[2].y * a));
+                w.w = Tr::pack2(opaque(pq[3].x * a), opaque(pq[3].y * a));
+                acc[u] = mfma16<Tr>(w, xv[c][q], acc[u]);
+            }
+            sched_fence();
+        }
+    };
+
+    if (steps > 0) copy_step(0, 0);  // in flight while the level table is filled
+    fill_lut_rw<512>(lut_all, tid);
+    wait_vmem();
+    __syncthreads();  // level table and step 0 ready
+    for (int j = 0; j < steps; ++j) {
+        const int b = j & 1;
+        if (j + 1 < steps) copy_step(j + 1, b ^ 1);
+        compute(j, b);
+        wait_vmem();
+        __syncthreads();  // step j + 1 landed; every wave is done with buffer b
+    }
+
+    // the slices' sums meet in LDS (the weight buffer of buffer 0): entry
+    // (slice, tile) of TW tiles per wave, 64 lanes
+    float4* red = reinterpret_cast<float4*>(bw(0));
+#pragma unroll
+    for (int u = 0; u < TW; ++u)
+        red[(s * T + t0 + u) * 64 + lane] = make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+    __syncthreads();
+    if (s != 0) return;
+    const int R = g.lora_rank;
+    const uint16_t* bias = reinterpret_cast<const uint16_t*>(g.bias);
+#pragma unroll
+    for (int u = 0; u < TW; ++u) {
+        float v[4] = {acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
+#pragma unroll
+        for (int sl = 1; sl < S; ++sl) {
+            const float4 o = red[(sl * T + t0 + u) * 64 + lane];
+            v[0] += o.x;
+            v[1] += o.y;
+            v[2] += o.z;
+            v[3] += o.w;
+        }
+        // C[4 h + i][r] of tile t0 + u: weight row n0 + 16 (t0 + u) + 4 h + i, activation row r
+        const int64_t m = r, nc = n0 + 16 * (t0 + u) + 4 * h;
+        if (m >= M || nc >= N) continue;  // N % 8 == 0: all four columns valid
+        if (R > 0) {  // R % 16 == 0; T, L 16-byte aligned: 8 ranks per load
+            const uint4* t8 =
+                reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(g.lora_x) + m * R);
+            const uint16_t* L = reinterpret_cast<const uint16_t*>(g.lora_w);
+            float l[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int k8 = 0; k8 < R / 8; ++k8) {
+                const uint4 tv = t8[k8];
+                const uint32_t tw[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 lv = reinterpret_cast<const uint4*>(L + (nc + i) * R)[k8];
+                    const uint32_t lw[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        l[i] += Tr::to_f32((uint16_t)(tw[q] & 0xFFFF)) * Tr::to_f32((uint16_t)(lw[q] & 0xFFFF));
+                        l[i] += Tr::to_f32((uint16_t)(tw[q] >> 16)) * Tr::to_f32((uint16_t)(lw[q] >> 16));
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += l[i];
+        }
+        if (bias) {
+            uint16_t bb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bb[i] = bias[nc + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += Tr::to_f32(bb[i]);
+        }
+        uint2 pk;
+        pk.x = Tr::pack2(v[0], v[1]);
+        pk.y = Tr::pack2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * N + nc) = pk;
+    }
+}
+
 // Sum of the split partials [splits][rows][cols] (+ bias) (+ T[row] . L[col]
 // over R ranks, when R > 0), one rounding; four columns per lane (cols % 4 == 0).
 template <typename Tr>
@@ -2476,10 +2731,12 @@ int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) 
     return backward ? plan(M, K, N, true, num_groups).splits : plan(M, N, K, false, num_groups).splits;
 }
 
+int gemv_ks_tiles(int64_t M, int64_t N, int64_t K);  // below, beside the forward dispatcher
+
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
     // small M: room for either kernel (a pinned tile kind skips the small-M one)
     int64_t gemv_need = 0;
-    if (!backward && use_gemv(M, num_groups)) {
+    if (!backward && use_gemv(M, num_groups) && !gemv_ks_tiles(M, N, K)) {
         const int sp = gemv_splits(M, N, K);
         gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
     }
@@ -2492,11 +2749,63 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
 #define STM_FWD_R8_AUTO 1
 #endif
 
+// 1: small-M forwards that fit k_gemv_ks run it (no split reduction).
+#ifndef STM_GEMV_KS
+#define STM_GEMV_KS 1
+#endif
+
+// Configuration of the split-free small-M forward (k_gemv_ks), encoded as
+// T | TW << 4 | XR << 8, or 0 when none applies: the activation rows must fit
+// (M <= XR) and the launch must keep three quarters of the CUs busy. Among the
+// fits, the least estimated time: rounds x (fixed cost + tile-groups per wave),
+// the fixed cost (level table, first copies) counted as one tile-group and a
+// tile-group of a one-tile wave as 1.25 (half the work between barriers).
+int gemv_ks_config(int64_t M, int64_t N, int64_t K) {
+    if (!STM_GEMV_KS || M < 1 || M > 16) return 0;
+    static const int cfgs[][3] = {{1, 1, 4}, {2, 1, 8}, {4, 1, 16}, {8, 1, 16}, {4, 2, 4}};
+    const int64_t groups = (K + GV_GK - 1) / GV_GK, cus = device_cus();
+    int best = 0;
+    double best_t = 1e30;
+    for (const auto& c : cfgs) {
+        const int T = c[0], TW = c[1], XR = c[2], S = 8 * TW / T;
+        if (M > XR) continue;
+        const int64_t blocks = (N + 16 * T - 1) / (16 * T);
+        if (blocks * 4 < cus * 3) continue;
+        const int64_t rounds = (blocks + cus - 1) / cus;
+        const double t = (double)rounds * (1.0 + (double)((groups + S - 1) / S) * TW * (TW == 1 ? 1.25 : 1.0));
+        if (t < best_t) best_t = t, best = T | TW << 4 | XR << 8;
+    }
+    return best;
+}
+int gemv_ks_tiles(int64_t M, int64_t N, int64_t K) { return gemv_ks_config(M, N, K); }
+
+int launch_gemv_ks(const GemmArgs& g, int cfg, int dtype, hipStream_t stream) {
+    const int T = cfg & 15;
+    const dim3 grid((unsigned)((g.N + 16 * T - 1) / (16 * T))), block(512);
+#define STM_KS_LAUNCH(TT, TW, XR)                                                           \
+    if (dtype == STM_BF16)                                                                  \
+        hipLaunchKernelGGL((k_gemv_ks<BF16, TT, TW, XR>), grid, block, 0, stream, g);       \
+    else                                                                                    \
+        hipLaunchKernelGGL((k_gemv_ks<F16, TT, TW, XR>), grid, block, 0, stream, g);
+    switch (cfg) {
+        case 1 | 1 << 4 | 4 << 8: STM_KS_LAUNCH(1, 1, 4) break;
+        case 2 | 1 << 4 | 8 << 8: STM_KS_LAUNCH(2, 1, 8) break;
+        case 4 | 1 << 4 | 16 << 8: STM_KS_LAUNCH(4, 1, 16) break;
+        case 8 | 1 << 4 | 16 << 8: STM_KS_LAUNCH(8, 1, 16) break;
+        case 4 | 2 << 4 | 4 << 8: STM_KS_LAUNCH(4, 2, 4) break;
+        default: return set_error(STM_ERR_INVALID, "gemm_fwd: small-M configuration %d", cfg);
+    }
+#undef STM_KS_LAUNCH
+    return check_launch("gemm_fwd (small M, one launch)");
+}
+
 int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     // small M: the weight-streaming kernel, when its partials have a workspace
     // (or it needs none) and the LoRA term can go to the reduce
     if (use_gemv(g.M, g.num_groups) && tile_override() < 0) {
+        const int kt = gemv_ks_tiles(g.M, g.N, g.K);
+        if (kt) return launch_gemv_ks(g, kt, dtype, stream);
         const int sp = gemv_splits(g.M, g.N, g.K);
         if (sp == 1 ? g.lora_rank == 0 : g.partial != nullptr) {
             g.splits = sp;

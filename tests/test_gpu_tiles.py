@@ -3,8 +3,10 @@
 The library picks, per call, the 256 x 256 tile (register-weight kernels, or
 LDS-weight kernels for some split reductions), the 128 x 256 register-weight
 tile (unsplit) or the 128 x 128 LDS-weight tile, split or not, and for a
-forward of at most 32 rows the weight-streaming small-M kernel (its reduction
-ranges summed by the split-reduce kernel, which adds bias and the LoRA term).
+forward of at most 32 rows a weight-streaming small-M kernel: the split-free one
+(its work-group's waves split the reduction and add bias and the LoRA term
+themselves) where the rows fit and the launch fills the GPU, else the one whose
+reduction ranges the split-reduce kernel sums (adding bias and the LoRA term).
 stm_nf4_gemm_set_tile pins the tile kind (and so skips the small-M kernel) and
 a call through the C ABI without a workspace pins "unsplit", so each kernel is
 reached on shapes whose rows, output columns and reduction are not multiples
@@ -123,6 +125,15 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (320, 520, 576, 64, True, 16),     # last 256-row tile: 64 rows (the 2-fragment short item)
     (384, 264, 640, 64, False, 0),     # last 256-row tile: 128 rows (the 4-fragment short item)
     (100, 256, 1024, 128, True, 16),   # one tile of 100 rows (4 fragments), blocksize 128
+    # the split-free small-M kernel (16 T weight rows per work-group, 8 / T reduction slices)
+    (1, 4096, 4096, 64, True, 16),     # T = 1: 8 slices, 2 steps; bias + LoRA in its epilogue
+    (4, 3072, 1600, 64, False, 0),     # T = 1 at its row limit, 192 work-groups, 7 groups (last 64 deep)
+    (2, 4096, 4160, 64, True, 0),      # T = 1: 17 groups, the third step holds one tail group
+    (8, 8192, 2048, 128, True, 16),    # T = 2 at its row limit, blocksize 128
+    (16, 12288, 1024, 64, True, 16),   # T = 4: 16 rows, 2 slices
+    (13, 25600, 1024, 512, False, 0),  # T = 8: one slice, blocksize 512 (one scale per group)
+    (2, 12288, 4096, 128, True, 16),   # T = 4, two tiles per wave, 4 slices; blocksize 128, bias + LoRA
+    (4, 14336, 4160, 64, False, 0),    # two tiles per wave: 17 groups, the last step holds one
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
