@@ -172,12 +172,18 @@ def test_gemm_workspace_sizing(L):
     # ways over the 224 steps of its 14336-long reduction
     assert L.stm_nf4_gemm_workspace_bytes(33, 14336, 4096, 0) == 2 * 33 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
-    # forward with M <= 16: the small-M kernel's ranges (blocks of 256 weight
-    # rows, one per CU; groups of 256 along K; fewest rounds x (3 + groups per
-    # range) + 6 for the reduce): 56 blocks x 16 groups -> 4 ranges of 4
-    # (224 work-groups, one round); 16 blocks x 56 groups -> 14 ranges of 4
-    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 4 * 16 * 14336 * 4
-    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 14 * 1 * 4096 * 4
+    # forward with M <= 16 where the split-free small-M kernel applies (the rows
+    # fit and it fills the GPU): no partials of its own, so the workspace is
+    # what a pinned tile kind would split: 16 rows of W [14336, 4096] -> the
+    # 128 x 128 tiles' 2 ways; 1 row of W [4096, 14336] -> 8 ways
+    assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 0) == 2 * 16 * 14336 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 8 * 1 * 4096 * 4
+    # 16 rows of W [4096, 14336] do not fit it (16 rows need 4 tiles per
+    # work-group: 64 work-groups): the split small-M kernel's ranges (blocks of
+    # 256 weight rows, one per CU; groups of 256 along K; fewest rounds x
+    # (3 + groups per range) + 6 for the reduce): 16 blocks x 56 groups -> 14
+    # ranges of 4
+    assert L.stm_nf4_gemm_workspace_bytes(16, 4096, 14336, 0) == 14 * 16 * 4096 * 4
     # 17..32 rows: blocks of 192 weight rows: 75 blocks x 16 groups -> 3 ranges
     # of 6 (225 work-groups, one round)
     assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 3 * 17 * 14336 * 4
