@@ -791,8 +791,9 @@ def run_mlp(torch, args):
 
 def run_small_m(torch, args):
     """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward (the
-    weight-streaming small-M kernel plus its split reduce) and input gradient
-    (split reduction over the tile kernel), against dequantize + hipBLASLt."""
+    split-free weight-streaming small-M kernel, one launch) and input gradient
+    (split reduction over the tile kernel), against dequantize + hipBLASLt; and
+    the fused forward of a single row (batch-1 decode)."""
     from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd
     dev = torch.device("cuda:0")
     N, K, M = 14336, 4096, 16
@@ -804,10 +805,14 @@ def run_small_m(torch, args):
     b = graph_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy, p, st.absmax, (N, K), 64), 20)
     uf = graph_time_ms(torch, lambda: x @ dequantize_4bit(p, st).t(), 20)
     ub = graph_time_ms(torch, lambda: dy @ dequantize_4bit(p, st), 20)
+    x1 = x[:1].contiguous()
+    f1 = graph_time_ms(torch, lambda: nf4_gemm_fwd(x1, p, st.absmax, (N, K), 64), 20)
     wbytes = N * K / 2 + 4 * N * K / 64
     return {"M": M, "fused_fwd_ms": round(f, 4), "fused_bwd_ms": round(b, 4), "unfused_fwd_ms": round(uf, 4),
             "unfused_bwd_ms": round(ub, 4), "fused_fwd_weight_gbs": round(wbytes / f / 1e6, 1),
-            "timing": "device time: 20 launches captured in one HIP graph, replayed (split reduce included)"}
+            "fused_fwd_m1_ms": round(f1, 4), "fused_fwd_m1_weight_gbs": round(wbytes / f1 / 1e6, 1),
+            "timing": "device time: 20 launches captured in one HIP graph, replayed (the input gradient's "
+                      "split reduce included)"}
 
 
 SECONDARY_CONFIGS = {
@@ -861,9 +866,9 @@ def run_profile(args):
 
 
 def run_profile_small_m(args):
-    """Kernel-only pass for rocprofv3 at decode size: the fused forward (small-M
-    kernel + split reduce) and input gradient at M = 16 on the 14336 x 4096
-    weight, each launched --kernel-reps times."""
+    """Kernel-only pass for rocprofv3 at decode size: the fused forward (the
+    split-free small-M kernel) and input gradient (tile kernel + split reduce)
+    at M = 16 on the 14336 x 4096 weight, each launched --kernel-reps times."""
     import torch
 
     from stratum_amd.functional import nf4_gemm_bwd_dx, nf4_gemm_fwd
