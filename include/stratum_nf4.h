@@ -111,9 +111,11 @@ int stm_nf4_dequantize_many(int count, const uint8_t* const* packed, const float
  *                  (small M) the reduction is split over several work-groups
  *                  whose fp32 partials go there and are summed (in a fixed
  *                  order) by a second kernel; NULL disables the split. For
- *                  M <= 32 a weight-streaming kernel runs instead of the tiles
+ *                  M <= 32 a weight-streaming kernel runs instead of the tiles:
+ *                  in one launch with no workspace where its split-free form
+ *                  fits (M <= 16 and enough weight rows to fill the GPU), else
  *                  when it has this workspace (or needs none: one range and no
- *                  LoRA term); its split reduce adds bias and the LoRA term.
+ *                  LoRA term), its split reduce adding bias and the LoRA term.
  *   constraints  : K % 64 == 0, K % blocksize == 0, all pointers 16-byte aligned
  */
 int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const void* bias, const void* T,
