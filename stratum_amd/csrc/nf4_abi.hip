@@ -295,6 +295,7 @@ int stm_nf4_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, 
     g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
     g.partial = need ? (float*)workspace : nullptr;
+    g.stream_out = M * N * 2 >= kStreamOutBytes;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 
@@ -325,6 +326,7 @@ int stm_nf4_gemm_fwd_noalloc(const void* X, const uint8_t* packed, const float* 
     g.lora_w = lora_rank ? L : nullptr; g.lora_rank = lora_rank; g.out = Y; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
     g.partial = need ? (float*)ws : nullptr;
+    g.stream_out = M * N * 2 >= kStreamOutBytes;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 
@@ -348,6 +350,7 @@ int stm_nf4_gemm_bwd_dx(const void* dY, const uint8_t* packed, const float* absm
     g.lora_w = lora_rank ? At : nullptr; g.lora_rank = lora_rank; g.out = dX; g.M = M; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = nullptr; g.num_groups = 1;
     g.partial = need ? (float*)workspace : nullptr;
+    g.stream_out = M * K * 2 >= kStreamOutBytes;
     return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
 }
 
@@ -393,6 +396,7 @@ int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* 
     g.a = X; g.packed = packed; g.absmax = absmax; g.out = Y; g.M = max_rows; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
     g.group_bm = host_offsets ? grouped_tile_rows(host_offsets, num_experts) : 0;
+    g.stream_out = host_offsets && (int64_t)host_offsets[num_experts] * N * 2 >= kStreamOutBytes;
     return launch_gemm_fwd(g, dtype, (hipStream_t)stream);
 }
 
@@ -413,6 +417,7 @@ int stm_nf4_grouped_gemm_bwd_dx(const void* dY, const uint8_t* packed, const flo
     GemmArgs g{};
     g.a = dY; g.packed = packed; g.absmax = absmax; g.out = dX; g.M = max_rows; g.N = N; g.K = K;
     g.blocksize = blocksize; g.offsets = offsets; g.num_groups = num_experts;
+    g.stream_out = host_offsets && (int64_t)host_offsets[num_experts] * K * 2 >= kStreamOutBytes;
     return launch_gemm_bwd(g, dtype, (hipStream_t)stream);
 }
 

@@ -89,6 +89,7 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk
 
 typedef __attribute__((address_space(3))) uint4 lds_uint4;
 typedef int v2i32_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t lds_offset(const uint4* p) {
     return (uint32_t)(size_t)((const lds_uint4*)(p));
@@ -505,7 +506,8 @@ __device__ __forceinline__ void store_tile_f32(const f32x16_t (&acc)[FA][FB], fl
 template <typename Tr, int FA, int FB, int CX = 0, int NP = 2>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FA][FB], uint16_t* __restrict__ out, int ld,
                                                int ocol_base, int ocols, int orow_base, int orows,
-                                               const uint16_t* __restrict__ bias, int lane, uint4* stage) {
+                                               const uint16_t* __restrict__ bias, int lane, uint4* stage,
+                                               bool nt = false) {
     static_assert(FB % NP == 0 && (FA == 1 || FA == 2 || FA == 4), "32, 64 or 128 columns per wave");
     // (the register-weight kernels use FA = 2, NP = 2; the LDS-weight kernels'
     // 128 x 128 tiles store a quarter of the bytes per item and measured no gain)
@@ -551,7 +553,13 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FA][FB], ui
             const int rr = RPI * it + lane / CH, c = lane % CH;
             const uint4 v = stage[rr * CH + (c ^ (rr & (CH - 1)))];
             const int orow = orow_base + p * RP + rr, col = ocol_base + 8 * c;
-            if (orow < orows && col < ocols) *reinterpret_cast<uint4*>(out + (orow * ld + col)) = v;
+            if (orow < orows && col < ocols) {
+                if (nt)
+                    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v),
+                                                reinterpret_cast<u32x4_t*>(out + (orow * ld + col)));
+                else
+                    *reinterpret_cast<uint4*>(out + (orow * ld + col)) = v;
+            }
         }
     }
 }
@@ -1202,7 +1210,7 @@ __global__ __launch_bounds__(256 * WM) void k_gemm_fwd_rw(GemmArgs g) {
         __syncthreads();  // every wave is done reading the activation buffers
         store_tile_lds<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
                                      (int)N, (int)(m0 + xrow0), (int)grp.rows,
-                                     reinterpret_cast<const uint16_t*>(g.bias), lane_e, stage);
+                                     reinterpret_cast<const uint16_t*>(g.bias), lane_e, stage, g.stream_out != 0);
     } else {
         store_tile_rw<Tr, 2, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
                                  (int)N, (int)(m0 + xrow0), (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias),
@@ -1355,7 +1363,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fwd_r8(GemmArgs g) {
         __syncthreads();  // every wave is done reading the activation buffers
         store_tile_lds<Tr, 1, FB>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * N, (int)N, (int)col_base,
                                      (int)N, (int)m0, (int)grp.rows, reinterpret_cast<const uint16_t*>(g.bias), lane_e,
-                                     stage);
+                                     stage, g.stream_out != 0);
     }
     __syncthreads();
     }
@@ -1810,7 +1818,7 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
         uint4* stage = (wave < PER_BUF ? sA0 + wave * RPW : sA1 + (wave - PER_BUF) * RPW);
         __syncthreads();  // every wave is done reading the dY buffers
         store_tile_lds<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
-                                        (int)K, (int)m0, (int)grp.rows, nullptr, lane_e, stage);
+                                        (int)K, (int)m0, (int)grp.rows, nullptr, lane_e, stage, g.stream_out != 0);
     } else {
         store_tile_rw<Tr, 2, FB, 1>(acc, reinterpret_cast<uint16_t*>(g.out) + grp.row0 * K, (int)K, (int)col_base,
                                     (int)K, (int)m0, (int)grp.rows, nullptr, lane_e);

@@ -33,7 +33,15 @@ struct GemmArgs {
     // Grouped forward: tile height chosen from the host's per-expert row counts
     // (grouped_tile_rows); 0 = the planner's 256-row tile.
     int group_bm;
+    // 1: the register-weight kernels write the output with non-temporal stores.
+    // Set for outputs of at least kStreamOutBytes: the next kernel would not
+    // find them in the 256 MB infinity cache anyway, and written back later
+    // they compete with that kernel's reads (the LoRA step's backward reads dY
+    // right after the forward wrote a 235 MB output: 1.2 % per step).
+    int stream_out;
 };
+
+constexpr int64_t kStreamOutBytes = 64ll << 20;
 
 // Split count the launchers use for a problem (1 = no split) and the fp32
 // workspace it needs: sized so that small-M problems still put >= 512
