@@ -2311,6 +2311,214 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
     }
 }
 
+// ----------------------------------------------------- small-M input gradient
+// dX[M, K] = dY[M, N] . W[N, K] for M <= 16 rows, bound by dequantizing the
+// streamed weight. A work-group owns 256 output columns k (128 bytes of every
+// packed weight row) and one range of weight rows n (the reduction), walked in
+// groups of 256 rows; each range writes fp32 partials [split][m][k] that
+// k_split_reduce sums (adding the LoRA term U . At^T). Wave w owns the columns
+// [32 w, 32 w + 32) of the block: two 16-column tiles of v_mfma_f32_16x16x32
+// (weight side: 16 columns x 32 rows n; dY side: 32 rows n x 16 activation
+// rows), the two 8-byte halves of 16-byte chunk w of every packed row.
+// Operands reach LDS through lane-contiguous global -> LDS copies,
+// double-buffered, one barrier per group:
+//  - packed weight: 256 rows x 128 bytes, chunk q of row r in slot q ^ key(r);
+//  - absmax: [column block][256 rows], dword copies of one row per lane;
+//  - dY: M rows x 256 n, piece p (8 values) of row m in slot p ^ m; rows
+//    M .. 15 are zeroed once and never copied.
+// The weight-side operand needs 8 consecutive n of one column per lane: a
+// ds_read_b64_tr_b4 of 16 rows x 16 columns, in which lane i of a 16-lane group
+// points at 8 bytes of row i and lane c receives nibble c of the 16 rows, row r
+// in nibble r. Nibble c is the low nibble of byte c / 2 for even c and packed
+// NF4 keeps the even column in the high nibble, so lane c holds column c ^ 1
+// (undone by the store). In 64-row subgroup u, lane group g reads rows
+// 64 u + 16 g + 0..15; the first word (rows 0..7) feeds the tile's first MFMA
+// and the second word (rows 8..15) its second, the dY operand taking the same
+// rows (the assignment of rows to reduction slots is free when both operands
+// agree). Each weight row has its own absmax, so a lane applies 16 per
+// subgroup (four broadcast 16-byte reads). The dequantization is the register
+// path of the other kernels: a perm-built level-table address per byte, an
+// fp32 product per element, one rounding.
+struct GbCfg {
+    static constexpr int KW = 256, GN = 256, XR = 16;
+    static constexpr int kLut = 256 * RW_LUT_COPIES * 8;
+    static constexpr int kW = GN * 128;    // packed rows of a group
+    static constexpr int kA = 4 * GN * 4;  // absmax, up to 4 column blocks
+    static constexpr int kX = XR * GN * 2; // dY rows of the group
+    static constexpr int kBuf = kW + kA + kX;
+    static constexpr int kLds = kLut + 2 * kBuf;
+    static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+template <typename Tr>
+__global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_split) {
+    using C = GbCfg;
+    constexpr int GN = C::GN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ __align__(16) uint8_t smem[C::kLds];
+    float2* lut_all = reinterpret_cast<float2*>(smem);
+    auto bw = [&](int b) { return reinterpret_cast<uint4*>(smem + C::kLut + b * C::kBuf); };  // [GN][8]
+    auto ba = [&](int b) { return reinterpret_cast<float*>(smem + C::kLut + b * C::kBuf + C::kW); };
+    auto bx = [&](int b) { return reinterpret_cast<uint4*>(smem + C::kLut + b * C::kBuf + C::kW + C::kA); };
+
+    const int64_t K = g.K, N = g.N, M = g.M;
+    const int bshift = 31 - __builtin_clz(g.blocksize);
+    const int64_t kblocks = K >> bshift;
+    const int nbw = (C::KW >> bshift) > 0 ? (C::KW >> bshift) : 1;  // column blocks of the work-group
+    const int ngroups = (int)((N + GN - 1) / GN);
+    const int z = blockIdx.y;
+    const int g_begin = z * groups_per_split;
+    const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
+    const int64_t k0 = (int64_t)blockIdx.x * C::KW, kb0 = k0 >> bshift;
+    const uint16_t* dy = reinterpret_cast<const uint16_t*>(g.a);
+    auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
+
+    // packed-weight copies: instruction 4 wave + j covers rows 8 (4 wave + j) + 0..7;
+    // the lane takes row 8 (4 wave + j) + lane / 8, chunk (lane % 8) ^ key(row)
+    // (chunks past K re-read the row's last one: they feed unstored columns)
+    int wrow[4];
+    int64_t wcol[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        wrow[j] = 8 * (4 * wave + j) + (lane >> 3);
+        const int64_t cb = k0 / 2 + 16 * ((lane & 7) ^ swz_key(wrow[j]));
+        wcol[j] = cb + 16 <= K / 2 ? cb : K / 2 - 16;
+    }
+    // dY copies: wave w copies rows 2 w (lanes 0..31) and 2 w + 1 (lanes 32..63)
+    // when they exist; the lane fills slot lane % 32 of its row, piece (lane % 32) ^ row
+    const int xm = 2 * wave + (lane >> 5);
+    const bool xon = xm < M;
+    const int xp = (lane & 31) ^ (xm & 15);
+    const uint16_t* xsrc = dy + (xon ? xm : 0) * N + 8 * xp;
+
+    auto copy_group = [&](int grp, int b) {
+        const int64_t n0 = (int64_t)grp * GN;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + wrow[j] < N ? n0 + wrow[j] : N - 1;
+            dma16(g.packed + n * (K / 2) + wcol[j], uniform(lds_offset(bw(b) + (4 * wave + j) * 64)));
+        }
+        // absmax: instruction i = wave + 8 j (< 4 nbw) covers block i / 4, rows 64 (i % 4) + lane
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = wave + 8 * j;
+            if (i < 4 * nbw) {
+                const int64_t n = n0 + 64 * (i & 3) + lane < N ? n0 + 64 * (i & 3) + lane : N - 1;
+                const int64_t kb = kb0 + (i >> 2) < kblocks ? kb0 + (i >> 2) : kblocks - 1;
+                dma4(g.absmax + n * kblocks + kb,
+                     uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(ba(b) + 64 * i))));
+            }
+        }
+        if (xon) dma16(xsrc + (n0 + 8 * xp < N ? n0 : -8 * xp), uniform(lds_offset(bx(b) + 64 * wave)));
+    };
+
+    const int c = lane & 15, gq = lane >> 4;
+    const uint32_t copy_off = 8u * (uint32_t)(lane & 31);
+    // transposed read of subgroup u, tile t: row 16 gq + c of the subgroup,
+    // chunk wave (slot wave ^ key(row), key(row) = c / 2 here), half t
+    const uint32_t tr_lane = 128u * (uint32_t)(16 * gq + c) + 16u * (uint32_t)(wave ^ (c >> 1));
+    const int wblk = (int)(((k0 + 32 * wave) >> bshift) - kb0);  // this wave's column block (< nbw)
+    f32x4_t acc[2];
+    acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // table reads of one transposed read: word wd, byte bb (rows 8 wd + 2 bb, + 1)
+    auto issue = [&](const v2i32_t& v, f32x2_t (&pp)[2][4]) {
+#pragma unroll
+        for (int wd = 0; wd < 2; ++wd) {
+            const uint32_t word = (uint32_t)(wd ? v.y : v.x);
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const uint32_t addr = __builtin_amdgcn_perm(copy_off, word, 0x0C0C0004u | ((uint32_t)bb << 8));
+                pp[wd][bb] = *(const __attribute__((address_space(3))) f32x2_t*)(size_t)addr;
+            }
+        }
+    };
+    // one group: items i = 2 u + t; the table reads of item i + 1 go out before
+    // item i's math. TAIL (the group reaching past N) zeroes the absmax and dY
+    // of subgroups past N.
+    auto compute = [&](int grp, int b, auto tail_c) {
+        constexpr bool TAIL = decltype(tail_c)::value;
+        const int64_t n0 = (int64_t)grp * GN;
+        const uint32_t wt = lds_offset(bw(b)) + tr_lane;
+        v2i32_t tr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            tr[i] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+                (__attribute__((address_space(3))) v2i32_t*)(size_t)(wt + 8192u * (uint32_t)(i >> 1) +
+                                                                     8u * (uint32_t)(i & 1)));
+        f32x2_t p[2][2][4];
+        f32x4_t av[4];
+        uint4 xv[2];
+        issue(tr[0], p[0]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int u = i >> 1, t = i & 1;
+            if (t == 0) {
+                const bool ok = !TAIL || n0 + 64 * u < N;
+                const float* ap = ba(b) + wblk * GN + 64 * u + 16 * gq;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(ap + 4 * q);
+                    av[q] = ok ? a : f32x4_t{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const uint4 v = bx(b)[c * 32 + ((8 * u + 2 * gq + s) ^ c)];
+                    xv[s] = ok ? v : make_uint4(0, 0, 0, 0);
+                }
+            }
+            if (i + 1 < 8) issue(tr[i + 1], p[(i + 1) & 1]);
+            sched_fence();
+#pragma unroll
+            for (int wd = 0; wd < 2; ++wd) {
+                // byte bb: row 8 wd + 2 bb in the low nibble (.y), row 8 wd + 2 bb + 1 in the high (.x)
+                const f32x2_t(&pq)[4] = p[i & 1][wd];
+                const f32x4_t a0 = av[2 * wd], a1 = av[2 * wd + 1];
+                uint4 w;
+                w.x = Tr::pack2(opaque(pq[0].y * a0[0]), opaque(pq[0].x * a0[1]));
+                w.y = Tr::pack2(opaque(pq[1].y * a0[2]), opaque(pq[1].x * a0[3]));
+                w.z = Tr::pack2(opaque(pq[2].y * a1[0]), opaque(pq[2].x * a1[1]));
+                w.w = Tr::pack2(opaque(pq[3].y * a1[2]), opaque(pq[3].x * a1[3]));
+                acc[t] = mfma16<Tr>(w, xv[wd], acc[t]);
+            }
+            sched_fence();
+        }
+    };
+
+    if (g_begin < g_end) copy_group(g_begin, 0);  // in flight while the tables are set up
+    for (int i = tid; i < 2 * C::XR * 32; i += 512) {  // dY rows M .. 15 of both buffers stay zero
+        const int s = i % (C::XR * 32);
+        if (s / 32 >= M) bx(i / (C::XR * 32))[s] = make_uint4(0, 0, 0, 0);
+    }
+    fill_lut_rw<512>(lut_all, tid);
+    wait_vmem();
+    __syncthreads();  // level table, zero rows and group g_begin ready
+    for (int grp = g_begin; grp < g_end; ++grp) {
+        const int b = (grp - g_begin) & 1;
+        if (grp + 1 < g_end) copy_group(grp + 1, b ^ 1);
+        if ((int64_t)(grp + 1) * GN > N)
+            compute(grp, b, std::true_type());
+        else
+            compute(grp, b, std::false_type());
+        wait_vmem();
+        __syncthreads();  // group grp + 1 landed; every wave is done with buffer b
+    }
+
+    // D[i][j] of tile t sits in lane j + 16 (i / 4), element i % 4: activation
+    // row j = lane % 16, A row i = 4 gq + e, i.e. column 16 t + ((4 gq + e) ^ 1)
+    // of this wave's 32
+    const int m = lane & 15;
+    if (m >= M) return;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int64_t col = k0 + 32 * wave + 16 * t + 4 * gq;
+        if (col < K)  // K % 64 == 0: all four columns valid
+            *reinterpret_cast<float4*>(g.partial + ((int64_t)z * M + m) * K + col) =
+                make_float4(acc[t][1], acc[t][0], acc[t][3], acc[t][2]);
+    }
+}
+
 // Sum of the split partials [splits][rows][cols] (+ bias) (+ T[row] . L[col]
 // over R ranks, when R > 0), one rounding; four columns per lane (cols % 4 == 0).
 template <typename Tr>
@@ -2741,6 +2949,32 @@ int gemm_splits(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) 
 
 int gemv_ks_tiles(int64_t M, int64_t N, int64_t K);  // below, beside the forward dispatcher
 
+// 1: small-M input gradients run k_gemv_bwd when the caller gives a workspace.
+#ifndef STM_GEMV_BWD
+#define STM_GEMV_BWD 1
+#endif
+
+bool use_gemv_bwd(int64_t M, int64_t N, int64_t K, int num_groups) {
+    return STM_GEMV_BWD && num_groups == 1 && M >= 1 && M <= GbCfg::XR && N > 0 && K > 0;
+}
+
+// Small-M input gradient: reduction ranges (in groups of 256 weight rows) that
+// minimise rounds x (fixed cost + groups per range) over the 256-column
+// work-groups; returns the range count and sets the groups per range.
+int gemv_bwd_splits(int64_t N, int64_t K, int* groups_per_split) {
+    const int64_t blocks = (K + GbCfg::KW - 1) / GbCfg::KW, groups = (N + GbCfg::GN - 1) / GbCfg::GN;
+    int64_t best_gps = groups > 0 ? groups : 1;
+    double best_t = 1e30;
+    for (int64_t sp = 1; sp <= groups && sp <= 64; ++sp) {
+        const int64_t gps = (groups + sp - 1) / sp, spe = (groups + gps - 1) / gps;
+        const int64_t rounds = (blocks * spe + kCUs - 1) / kCUs;
+        const double t = (double)rounds * (STM_GEMV_T_LAT + (double)gps);
+        if (t < best_t - 1e-9) best_t = t, best_gps = gps;
+    }
+    if (groups_per_split) *groups_per_split = (int)best_gps;
+    return groups > 0 ? (int)((groups + best_gps - 1) / best_gps) : 1;  // every range non-empty
+}
+
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int num_groups) {
     // small M: room for either kernel (a pinned tile kind skips the small-M one)
     int64_t gemv_need = 0;
@@ -2748,6 +2982,8 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
         const int sp = gemv_splits(M, N, K);
         gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
     }
+    if (backward && use_gemv_bwd(M, N, K, num_groups))  // partials even for one range (the reduce adds LoRA)
+        gemv_need = (int64_t)gemv_bwd_splits(N, K, nullptr) * M * K * (int64_t)sizeof(float);
     const int sp = gemm_splits(M, N, K, backward, num_groups);
     const int64_t need = sp > 1 ? (int64_t)sp * M * (backward ? K : N) * (int64_t)sizeof(float) : 0;
     return need > gemv_need ? need : gemv_need;
@@ -2810,8 +3046,9 @@ int launch_gemv_ks(const GemmArgs& g, int cfg, int dtype, hipStream_t stream) {
 int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
     // small M: the weight-streaming kernel, when its partials have a workspace
-    // (or it needs none) and the LoRA term can go to the reduce
-    if (use_gemv(g.M, g.num_groups) && tile_override() < 0) {
+    // (or it needs none) and the LoRA term can go to the reduce; not for a
+    // grouped call (its rows come from the offsets, even with one expert)
+    if (!g.offsets && use_gemv(g.M, g.num_groups) && tile_override() < 0) {
         const int kt = gemv_ks_tiles(g.M, g.N, g.K);
         if (kt) return launch_gemv_ks(g, kt, dtype, stream);
         const int sp = gemv_splits(g.M, g.N, g.K);
@@ -2844,7 +3081,24 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     return launch_split_reduce(g, g.N, g.bias, dtype, stream);
 }
 
+int launch_gemv_bwd(GemmArgs g, int dtype, hipStream_t stream) {
+    int gps = 1;
+    g.splits = gemv_bwd_splits(g.N, g.K, &gps);
+    const dim3 grid((unsigned)((g.K + GbCfg::KW - 1) / GbCfg::KW), (unsigned)g.splits), block(512);
+    if (dtype == STM_BF16)
+        hipLaunchKernelGGL((k_gemv_bwd<BF16>), grid, block, 0, stream, g, gps);
+    else
+        hipLaunchKernelGGL((k_gemv_bwd<F16>), grid, block, 0, stream, g, gps);
+    const int rc = check_launch("gemm_bwd_dx (small M)");
+    if (rc != STM_OK) return rc;
+    return launch_split_reduce(g, g.K, nullptr, dtype, stream, true);
+}
+
 int launch_gemm_bwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
+    // small M: the weight-streaming kernel when the caller gives a workspace for
+    // its partials (sized by gemm_workspace_bytes)
+    if (!g0.offsets && use_gemv_bwd(g0.M, g0.N, g0.K, g0.num_groups) && g0.partial && tile_override() < 0)
+        return launch_gemv_bwd(g0, dtype, stream);
     GemmArgs g = g0;
     const Plan p = plan(g.M, g.K, g.N, true, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;

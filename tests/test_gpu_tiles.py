@@ -171,6 +171,14 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
     (320, 512, 576, 64, 16),           # last 256-row tile: 64 rows (the 2-fragment short item)
     (384, 256, 640, 64, 0),            # last 256-row tile: 128 rows (the 4-fragment short item)
     (100, 1024, 256, 128, 16),         # one tile of 100 rows (4 fragments), blocksize 128
+    # the small-M input gradient (256 output columns per work-group, ranges of 256 weight rows)
+    (1, 4096, 4096, 64, 16),           # 16 ranges of one group, LoRA in the reduce
+    (16, 14336, 1024, 64, 0),          # 16 rows, 56 groups over uneven ranges
+    (5, 4160, 320, 64, 16),            # last group 64 rows (three subgroups past N); 320 columns: second block 64 wide
+    (3, 4160, 384, 128, 0),            # blocksize 128 (two scales per work-group row), second block 128 wide
+    (9, 448, 768, 256, 0),             # one range: groups of 256 and 192 rows; blocksize 256
+    (12, 1024, 4608, 512, 16),         # blocksize 512 (one scale per work-group row), 18 column blocks
+    (2, 64, 64, 64, 0),                # one subgroup of one group, one 64-column block
 ])
 def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
     from stratum_amd import _lib
@@ -193,6 +201,34 @@ def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank
     first = results["big-unsplit"]
     for name, dx in results.items():
         assert rel(dx, first) <= TOL[dtype] / 4, name
+
+
+@pytest.mark.parametrize("backward", [False, True])
+def test_grouped_call_with_one_expert_writes_only_its_rows(cuda, backward):
+    """A grouped call with one expert of 5 rows and max_rows 16 (a bound, not
+    the row count) runs a grouped kernel, which takes its rows from the offsets:
+    the output rows past offsets[1] keep their contents, and the 5 rows match
+    the fp32 reference. (The small-M kernels take their rows from M and are not
+    used for grouped calls.)"""
+    from stratum_amd import _lib
+    from stratum_amd.functional import _gemm_dtype
+    L = _lib.lib()
+    dtype, rows, max_rows, N, K = torch.bfloat16, 5, 16, 512, 256
+    rp, ra, wq = nf4((N, K), 77, 64, dtype)
+    packed, absmax = rp.to(cuda), ra.to(cuda)
+    a = seeded((max_rows, K if not backward else N), 12, 1.0, dtype).to(cuda)
+    out_cols = K if backward else N
+    out = torch.full((max_rows, out_cols), 7.0, dtype=dtype, device=cuda)
+    host = torch.tensor([0, rows], dtype=torch.int32)
+    dev_off = host.to(cuda)
+    fn = L.stm_nf4_grouped_gemm_bwd_dx if backward else L.stm_nf4_grouped_gemm_fwd
+    rc = fn(a.data_ptr(), packed.data_ptr(), absmax.data_ptr(), dev_off.data_ptr(), host.data_ptr(), 1, max_rows,
+            out.data_ptr(), N, K, 64, _gemm_dtype(a), _lib.stream_handle(cuda))
+    assert rc == 0, L.stm_last_error()
+    torch.cuda.synchronize()
+    ref = a[:rows].float() @ (wq.to(cuda) if backward else wq.to(cuda).t().contiguous())
+    assert rel(out[:rows], ref) <= TOL[dtype]
+    assert bool((out[rows:] == 7.0).all())
 
 
 @pytest.mark.parametrize("tile", ["big", "big8", "mid", "small"])
