@@ -2367,10 +2367,19 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
     const int64_t kblocks = K >> bshift;
     const int nbw = (C::KW >> bshift) > 0 ? (C::KW >> bshift) : 1;  // column blocks of the work-group
     const int ngroups = (int)((N + GN - 1) / GN);
-    const int z = blockIdx.y;
+    // tile T = z nb + x (column block x of range z). The hardware deals
+    // consecutive work-groups to the 8 XCDs in turn, so work-group L runs tile
+    // (L % 8) q + L / 8 of the 8 q launched: each XCD gets a contiguous run of
+    // column blocks of one range, which share the absmax lines and dY rows in
+    // its L2 (dealt round-robin, every absmax line went to all 8 XCDs).
+    const int nb = (int)((K + C::KW - 1) / C::KW), splits = (ngroups + groups_per_split - 1) / groups_per_split;
+    const int q8 = (int)(gridDim.x / 8);
+    const int T = (int)(blockIdx.x % 8) * q8 + (int)(blockIdx.x / 8);
+    if (T >= nb * splits) return;
+    const int z = T / nb;
     const int g_begin = z * groups_per_split;
     const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
-    const int64_t k0 = (int64_t)blockIdx.x * C::KW, kb0 = k0 >> bshift;
+    const int64_t k0 = (int64_t)(T % nb) * C::KW, kb0 = k0 >> bshift;
     const uint16_t* dy = reinterpret_cast<const uint16_t*>(g.a);
     auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
 
@@ -3084,7 +3093,8 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
 int launch_gemv_bwd(GemmArgs g, int dtype, hipStream_t stream) {
     int gps = 1;
     g.splits = gemv_bwd_splits(g.N, g.K, &gps);
-    const dim3 grid((unsigned)((g.K + GbCfg::KW - 1) / GbCfg::KW), (unsigned)g.splits), block(512);
+    const int64_t tiles = (g.K + GbCfg::KW - 1) / GbCfg::KW * g.splits;  // k_gemv_bwd deals them per XCD
+    const dim3 grid((unsigned)((tiles + 7) / 8 * 8)), block(512);
     if (dtype == STM_BF16)
         hipLaunchKernelGGL((k_gemv_bwd<BF16>), grid, block, 0, stream, g, gps);
     else
