@@ -792,7 +792,8 @@ def run_mlp(torch, args):
 def run_small_m(torch, args):
     """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward (the
     split-free weight-streaming small-M kernel, one launch) and input gradient
-    (split reduction over the tile kernel), against dequantize + hipBLASLt; and
+    (the weight-streaming small-M input-gradient kernel over ranges of weight
+    rows, plus the split reduce), against dequantize + hipBLASLt; and
     the fused forward of a single row (batch-1 decode)."""
     from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd
     dev = torch.device("cuda:0")
@@ -810,6 +811,7 @@ def run_small_m(torch, args):
     wbytes = N * K / 2 + 4 * N * K / 64
     return {"M": M, "fused_fwd_ms": round(f, 4), "fused_bwd_ms": round(b, 4), "unfused_fwd_ms": round(uf, 4),
             "unfused_bwd_ms": round(ub, 4), "fused_fwd_weight_gbs": round(wbytes / f / 1e6, 1),
+            "fused_bwd_weight_gbs": round(wbytes / b / 1e6, 1),
             "fused_fwd_m1_ms": round(f1, 4), "fused_fwd_m1_weight_gbs": round(wbytes / f1 / 1e6, 1),
             "timing": "device time: 20 launches captured in one HIP graph, replayed (the input gradient's "
                       "split reduce included)"}
@@ -867,7 +869,7 @@ def run_profile(args):
 
 def run_profile_small_m(args):
     """Kernel-only pass for rocprofv3 at decode size: the fused forward (the
-    split-free small-M kernel) and input gradient (tile kernel + split reduce)
+    split-free small-M kernel) and input gradient (small-M kernel + split reduce)
     at M = 16 on the 14336 x 4096 weight, each launched --kernel-reps times."""
     import torch
 
