@@ -2312,20 +2312,21 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
 }
 
 // ----------------------------------------------------- small-M input gradient
-// dX[M, K] = dY[M, N] . W[N, K] for M <= 16 rows, bound by dequantizing the
+// dX[M, K] = dY[M, N] . W[N, K] for M <= 32 rows, bound by dequantizing the
 // streamed weight. A work-group owns 256 output columns k (128 bytes of every
 // packed weight row) and one range of weight rows n (the reduction), walked in
-// groups of 256 rows; each range writes fp32 partials [split][m][k] that
-// k_split_reduce sums (adding the LoRA term U . At^T). Wave w owns the columns
-// [32 w, 32 w + 32) of the block: two 16-column tiles of v_mfma_f32_16x16x32
-// (weight side: 16 columns x 32 rows n; dY side: 32 rows n x 16 activation
-// rows), the two 8-byte halves of 16-byte chunk w of every packed row.
+// groups of GN rows (256, or 128 for 17..32 rows, whose doubled dY buffers
+// must fit); each range writes fp32 partials [split][m][k] that k_split_reduce
+// sums (adding the LoRA term U . At^T). Wave w owns the columns [32 w, 32 w + 32)
+// of the block: two 16-column tiles of v_mfma_f32_16x16x32 (weight side: 16
+// columns x 32 rows n; dY side: 32 rows n x 16 activation rows, MB blocks of
+// them), the two 8-byte halves of 16-byte chunk w of every packed row.
 // Operands reach LDS through lane-contiguous global -> LDS copies,
 // double-buffered, one barrier per group:
-//  - packed weight: 256 rows x 128 bytes, chunk q of row r in slot q ^ key(r);
-//  - absmax: [column block][256 rows], dword copies of one row per lane;
-//  - dY: M rows x 256 n, piece p (8 values) of row m in slot p ^ m; rows
-//    M .. 15 are zeroed once and never copied.
+//  - packed weight: GN rows x 128 bytes, chunk q of row r in slot q ^ key(r);
+//  - absmax: [column block][GN rows], dword copies of one row per lane;
+//  - dY: M rows x GN n, piece p (8 values) of row m in slot p ^ (m % 16); rows
+//    M .. XR - 1 are zeroed once and never copied.
 // The weight-side operand needs 8 consecutive n of one column per lane: a
 // ds_read_b64_tr_b4 of 16 rows x 16 columns, in which lane i of a 16-lane group
 // points at 8 bytes of row i and lane c receives nibble c of the 16 rows, row r
@@ -2339,8 +2340,11 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
 // subgroup (four broadcast 16-byte reads). The dequantization is the register
 // path of the other kernels: a perm-built level-table address per byte, an
 // fp32 product per element, one rounding.
+template <int MB>
 struct GbCfg {
-    static constexpr int KW = 256, GN = 256, XR = 16;
+    static constexpr int KW = 256, GN = MB == 1 ? 256 : 128, XR = 16 * MB;
+    static constexpr int NSUB = GN / 64;   // 64-row subgroups per group
+    static constexpr int PR = GN / 8;      // 16-byte dY pieces per row and group
     static constexpr int kLut = 256 * RW_LUT_COPIES * 8;
     static constexpr int kW = GN * 128;    // packed rows of a group
     static constexpr int kA = 4 * GN * 4;  // absmax, up to 4 column blocks
@@ -2348,12 +2352,15 @@ struct GbCfg {
     static constexpr int kBuf = kW + kA + kX;
     static constexpr int kLds = kLut + 2 * kBuf;
     static_assert(kLds <= 160 * 1024, "LDS");
+    static_assert(XR * PR == 512, "one dY copy per wave and group");
+    static_assert(PR <= 32 && (PR & (PR - 1)) == 0, "piece swizzle");
 };
+constexpr int GB_MAX_M = 32;
 
-template <typename Tr>
+template <typename Tr, int MB>
 __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_split) {
-    using C = GbCfg;
-    constexpr int GN = C::GN;
+    using C = GbCfg<MB>;
+    constexpr int GN = C::GN, NSUB = C::NSUB, PR = C::PR, NI = 2 * NSUB;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ __align__(16) uint8_t smem[C::kLds];
@@ -2383,38 +2390,40 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
     const uint16_t* dy = reinterpret_cast<const uint16_t*>(g.a);
     auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
 
-    // packed-weight copies: instruction 4 wave + j covers rows 8 (4 wave + j) + 0..7;
-    // the lane takes row 8 (4 wave + j) + lane / 8, chunk (lane % 8) ^ key(row)
+    // packed-weight copies: instruction NSUB wave + j covers rows 8 (NSUB wave + j) + 0..7;
+    // the lane takes row 8 (NSUB wave + j) + lane / 8, chunk (lane % 8) ^ key(row)
     // (chunks past K re-read the row's last one: they feed unstored columns)
-    int wrow[4];
-    int64_t wcol[4];
+    int wrow[NSUB];
+    int64_t wcol[NSUB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        wrow[j] = 8 * (4 * wave + j) + (lane >> 3);
+    for (int j = 0; j < NSUB; ++j) {
+        wrow[j] = 8 * (NSUB * wave + j) + (lane >> 3);
         const int64_t cb = k0 / 2 + 16 * ((lane & 7) ^ swz_key(wrow[j]));
         wcol[j] = cb + 16 <= K / 2 ? cb : K / 2 - 16;
     }
-    // dY copies: wave w copies rows 2 w (lanes 0..31) and 2 w + 1 (lanes 32..63)
-    // when they exist; the lane fills slot lane % 32 of its row, piece (lane % 32) ^ row
-    const int xm = 2 * wave + (lane >> 5);
+    // dY copies: wave w copies rows (64 / PR) w + 0.. when they exist; the lane
+    // fills slot lane % PR of row (64 / PR) w + lane / PR, piece (lane % PR) ^ (row % 16)
+    const int xm = (64 / PR) * wave + lane / PR;
     const bool xon = xm < M;
-    const int xp = (lane & 31) ^ (xm & 15);
+    const int xp = (lane % PR) ^ (xm & 15);
     const uint16_t* xsrc = dy + (xon ? xm : 0) * N + 8 * xp;
 
     auto copy_group = [&](int grp, int b) {
         const int64_t n0 = (int64_t)grp * GN;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NSUB; ++j) {
             const int64_t n = n0 + wrow[j] < N ? n0 + wrow[j] : N - 1;
-            dma16(g.packed + n * (K / 2) + wcol[j], uniform(lds_offset(bw(b) + (4 * wave + j) * 64)));
+            dma16(g.packed + n * (K / 2) + wcol[j], uniform(lds_offset(bw(b) + (NSUB * wave + j) * 64)));
         }
-        // absmax: instruction i = wave + 8 j (< 4 nbw) covers block i / 4, rows 64 (i % 4) + lane
+        // absmax: instruction i = wave + 8 j (< NSUB nbw) covers block i / NSUB,
+        // rows 64 (i % NSUB) + lane
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int i = wave + 8 * j;
-            if (i < 4 * nbw) {
-                const int64_t n = n0 + 64 * (i & 3) + lane < N ? n0 + 64 * (i & 3) + lane : N - 1;
-                const int64_t kb = kb0 + (i >> 2) < kblocks ? kb0 + (i >> 2) : kblocks - 1;
+            if (i < NSUB * nbw) {
+                const int64_t r = n0 + 64 * (i % NSUB) + lane;
+                const int64_t n = r < N ? r : N - 1;
+                const int64_t kb = kb0 + i / NSUB < kblocks ? kb0 + i / NSUB : kblocks - 1;
                 dma4(g.absmax + n * kblocks + kb,
                      uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(ba(b) + 64 * i))));
             }
@@ -2428,8 +2437,11 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
     // chunk wave (slot wave ^ key(row), key(row) = c / 2 here), half t
     const uint32_t tr_lane = 128u * (uint32_t)(16 * gq + c) + 16u * (uint32_t)(wave ^ (c >> 1));
     const int wblk = (int)(((k0 + 32 * wave) >> bshift) - kb0);  // this wave's column block (< nbw)
-    f32x4_t acc[2];
-    acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[2][MB];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // table reads of one transposed read: word wd, byte bb (rows 8 wd + 2 bb, + 1)
     auto issue = [&](const v2i32_t& v, f32x2_t (&pp)[2][4]) {
@@ -2450,18 +2462,18 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
         constexpr bool TAIL = decltype(tail_c)::value;
         const int64_t n0 = (int64_t)grp * GN;
         const uint32_t wt = lds_offset(bw(b)) + tr_lane;
-        v2i32_t tr[8];
+        v2i32_t tr[NI];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < NI; ++i)
             tr[i] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
                 (__attribute__((address_space(3))) v2i32_t*)(size_t)(wt + 8192u * (uint32_t)(i >> 1) +
                                                                      8u * (uint32_t)(i & 1)));
         f32x2_t p[2][2][4];
         f32x4_t av[4];
-        uint4 xv[2];
+        uint4 xv[2][MB];
         issue(tr[0], p[0]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const int u = i >> 1, t = i & 1;
             if (t == 0) {
                 const bool ok = !TAIL || n0 + 64 * u < N;
@@ -2472,12 +2484,14 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
                     av[q] = ok ? a : f32x4_t{0.f, 0.f, 0.f, 0.f};
                 }
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const uint4 v = bx(b)[c * 32 + ((8 * u + 2 * gq + s) ^ c)];
-                    xv[s] = ok ? v : make_uint4(0, 0, 0, 0);
-                }
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        const uint4 v = bx(b)[(16 * mb + c) * PR + ((8 * u + 2 * gq + s) ^ c)];
+                        xv[s][mb] = ok ? v : make_uint4(0, 0, 0, 0);
+                    }
             }
-            if (i + 1 < 8) issue(tr[i + 1], p[(i + 1) & 1]);
+            if (i + 1 < NI) issue(tr[i + 1], p[(i + 1) & 1]);
             sched_fence();
 #pragma unroll
             for (int wd = 0; wd < 2; ++wd) {
@@ -2489,16 +2503,17 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
                 w.y = Tr::pack2(opaque(pq[1].y * a0[2]), opaque(pq[1].x * a0[3]));
                 w.z = Tr::pack2(opaque(pq[2].y * a1[0]), opaque(pq[2].x * a1[1]));
                 w.w = Tr::pack2(opaque(pq[3].y * a1[2]), opaque(pq[3].x * a1[3]));
-                acc[t] = mfma16<Tr>(w, xv[wd], acc[t]);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[t][mb] = mfma16<Tr>(w, xv[wd][mb], acc[t][mb]);
             }
             sched_fence();
         }
     };
 
     if (g_begin < g_end) copy_group(g_begin, 0);  // in flight while the tables are set up
-    for (int i = tid; i < 2 * C::XR * 32; i += 512) {  // dY rows M .. 15 of both buffers stay zero
-        const int s = i % (C::XR * 32);
-        if (s / 32 >= M) bx(i / (C::XR * 32))[s] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < 2 * C::XR * PR; i += 512) {  // dY rows M .. XR - 1 of both buffers stay zero
+        const int s = i % (C::XR * PR);
+        if (s / PR >= M) bx(i / (C::XR * PR))[s] = make_uint4(0, 0, 0, 0);
     }
     fill_lut_rw<512>(lut_all, tid);
     wait_vmem();
@@ -2514,17 +2529,20 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
         __syncthreads();  // group grp + 1 landed; every wave is done with buffer b
     }
 
-    // D[i][j] of tile t sits in lane j + 16 (i / 4), element i % 4: activation
-    // row j = lane % 16, A row i = 4 gq + e, i.e. column 16 t + ((4 gq + e) ^ 1)
-    // of this wave's 32
-    const int m = lane & 15;
-    if (m >= M) return;
+    // D[i][j] of tile t, block mb sits in lane j + 16 (i / 4), element i % 4:
+    // activation row 16 mb + j (j = lane % 16), A row i = 4 gq + e, i.e. column
+    // 16 t + ((4 gq + e) ^ 1) of this wave's 32
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int64_t col = k0 + 32 * wave + 16 * t + 4 * gq;
-        if (col < K)  // K % 64 == 0: all four columns valid
-            *reinterpret_cast<float4*>(g.partial + ((int64_t)z * M + m) * K + col) =
-                make_float4(acc[t][1], acc[t][0], acc[t][3], acc[t][2]);
+    for (int mb = 0; mb < MB; ++mb) {
+        const int m = 16 * mb + (lane & 15);
+        if (m >= M) continue;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t col = k0 + 32 * wave + 16 * t + 4 * gq;
+            if (col < K)  // K % 64 == 0: all four columns valid
+                *reinterpret_cast<float4*>(g.partial + ((int64_t)z * M + m) * K + col) =
+                    make_float4(acc[t][mb][1], acc[t][mb][0], acc[t][mb][3], acc[t][mb][2]);
+        }
     }
 }
 
@@ -2964,14 +2982,15 @@ int gemv_ks_tiles(int64_t M, int64_t N, int64_t K);  // below, beside the forwar
 #endif
 
 bool use_gemv_bwd(int64_t M, int64_t N, int64_t K, int num_groups) {
-    return STM_GEMV_BWD && num_groups == 1 && M >= 1 && M <= GbCfg::XR && N > 0 && K > 0;
+    return STM_GEMV_BWD && num_groups == 1 && M >= 1 && M <= GB_MAX_M && N > 0 && K > 0;
 }
 
-// Small-M input gradient: reduction ranges (in groups of 256 weight rows) that
-// minimise rounds x (fixed cost + groups per range) over the 256-column
-// work-groups; returns the range count and sets the groups per range.
-int gemv_bwd_splits(int64_t N, int64_t K, int* groups_per_split) {
-    const int64_t blocks = (K + GbCfg::KW - 1) / GbCfg::KW, groups = (N + GbCfg::GN - 1) / GbCfg::GN;
+// Small-M input gradient: reduction ranges (in groups of 256 weight rows, 128
+// above 16 rows) that minimise rounds x (fixed cost + groups per range) over the
+// 256-column work-groups; returns the range count and sets the groups per range.
+int gemv_bwd_splits(int64_t M, int64_t N, int64_t K, int* groups_per_split) {
+    const int64_t gn = M <= 16 ? GbCfg<1>::GN : GbCfg<2>::GN;
+    const int64_t blocks = (K + GbCfg<1>::KW - 1) / GbCfg<1>::KW, groups = (N + gn - 1) / gn;
     int64_t best_gps = groups > 0 ? groups : 1;
     double best_t = 1e30;
     for (int64_t sp = 1; sp <= groups && sp <= 64; ++sp) {
@@ -2992,7 +3011,7 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
         gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
     }
     if (backward && use_gemv_bwd(M, N, K, num_groups))  // partials even for one range (the reduce adds LoRA)
-        gemv_need = (int64_t)gemv_bwd_splits(N, K, nullptr) * M * K * (int64_t)sizeof(float);
+        gemv_need = (int64_t)gemv_bwd_splits(M, N, K, nullptr) * M * K * (int64_t)sizeof(float);
     const int sp = gemm_splits(M, N, K, backward, num_groups);
     const int64_t need = sp > 1 ? (int64_t)sp * M * (backward ? K : N) * (int64_t)sizeof(float) : 0;
     return need > gemv_need ? need : gemv_need;
@@ -3092,13 +3111,20 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
 
 int launch_gemv_bwd(GemmArgs g, int dtype, hipStream_t stream) {
     int gps = 1;
-    g.splits = gemv_bwd_splits(g.N, g.K, &gps);
-    const int64_t tiles = (g.K + GbCfg::KW - 1) / GbCfg::KW * g.splits;  // k_gemv_bwd deals them per XCD
+    g.splits = gemv_bwd_splits(g.M, g.N, g.K, &gps);
+    const int64_t tiles = (g.K + GbCfg<1>::KW - 1) / GbCfg<1>::KW * g.splits;  // k_gemv_bwd deals them per XCD
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8)), block(512);
-    if (dtype == STM_BF16)
-        hipLaunchKernelGGL((k_gemv_bwd<BF16>), grid, block, 0, stream, g, gps);
-    else
-        hipLaunchKernelGGL((k_gemv_bwd<F16>), grid, block, 0, stream, g, gps);
+    if (g.M <= 16) {
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_bwd<BF16, 1>), grid, block, 0, stream, g, gps);
+        else
+            hipLaunchKernelGGL((k_gemv_bwd<F16, 1>), grid, block, 0, stream, g, gps);
+    } else {
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_bwd<BF16, 2>), grid, block, 0, stream, g, gps);
+        else
+            hipLaunchKernelGGL((k_gemv_bwd<F16, 2>), grid, block, 0, stream, g, gps);
+    }
     const int rc = check_launch("gemm_bwd_dx (small M)");
     if (rc != STM_OK) return rc;
     return launch_split_reduce(g, g.K, nullptr, dtype, stream, true);

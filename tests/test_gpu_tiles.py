@@ -179,6 +179,10 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
     (9, 448, 768, 256, 0),             # one range: groups of 256 and 192 rows; blocksize 256
     (12, 1024, 4608, 512, 16),         # blocksize 512 (one scale per work-group row), 18 column blocks
     (2, 64, 64, 64, 0),                # one subgroup of one group, one 64-column block
+    (17, 64, 64, 64, 0),               # 32-row variant (groups of 128 rows): one subgroup
+    (24, 4160, 320, 64, 16),           # 32-row variant: last group 64 rows, LoRA in the reduce
+    (32, 14336, 1024, 128, 0),         # 32-row variant at its row limit, blocksize 128
+    (20, 448, 768, 256, 16),           # 32-row variant: groups of 128 and 64 rows, blocksize 256
 ])
 def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
     from stratum_amd import _lib
