@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 METRIC = "NF4 dequant GB/s (% HBM peak); fused NF4-GEMM TFLOP/s (% MFMA peak)"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+EV_EVERY = 3  # timed steps per sampled one (HIP events around its fused GEMM launches)
 
 
 def seeded(torch, shape, seed, std, dtype, device):
@@ -258,25 +259,35 @@ def run_lora_step(args):
         A.grad = None
         B.grad = None
 
+    # every EV_EVERY-th timed step (from the first) is a sampled one: its fused GEMM
+    # launches are bracketed by HIP events (see below)
+    sampled = {"on": False}
+
     def timed_steps(n):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(n):
+        for i in range(n):
+            sampled["on"] = i % EV_EVERY == 0
             step()
+        sampled["on"] = False
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
     # The headline measures the fused dequant-GEMMs (forced for every row count);
     # the library default for this M (dequantize + hipBLASLt) is reported beside it.
-    # During the timed steps each fused GEMM launch is bracketed by HIP events on
-    # the stream it is launched on: the roofline's kernel duration is the mean
-    # over the timed region itself.
+    # During the sampled timed steps each fused GEMM launch is bracketed by HIP
+    # events on the stream it is launched on: the roofline's kernel duration is the
+    # mean over those launches of the timed region itself. Only every EV_EVERY-th
+    # step is sampled because each timing event holds the next launch back by
+    # about 5 us (four per step cost 0.8 % of the step, A/B-timed).
     import importlib
     NL = importlib.import_module("stratum_amd.nf4_linear")  # the package also exports a function of that name
     spans = {"fwd": [], "bwd": []}
 
     def bracketed(fn, key):
         def call(*a, **kw):
+            if not sampled["on"]:
+                return fn(*a, **kw)
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
             out = fn(*a, **kw)
@@ -350,9 +361,10 @@ def run_lora_step(args):
 
     xd = x.detach()
     reps = max(5, args.kernel_reps)
-    assert len(spans["fwd"]) == len(spans["bwd"]) == args.steps, {k: len(v) for k, v in spans.items()}
-    fwd_ms = sum(a.elapsed_time(b) for a, b in spans["fwd"]) / args.steps
-    bwd_ms = sum(a.elapsed_time(b) for a, b in spans["bwd"]) / args.steps
+    n_sampled = (args.steps + EV_EVERY - 1) // EV_EVERY
+    assert len(spans["fwd"]) == len(spans["bwd"]) == n_sampled, {k: len(v) for k, v in spans.items()}
+    fwd_ms = sum(a.elapsed_time(b) for a, b in spans["fwd"]) / n_sampled
+    bwd_ms = sum(a.elapsed_time(b) for a, b in spans["bwd"]) / n_sampled
     gemm_flops = 2.0 * M * N * K
     fwd_tf = gemm_flops / (fwd_ms * 1e-3) / 1e12
     bwd_tf = gemm_flops / (bwd_ms * 1e-3) / 1e12
@@ -413,7 +425,8 @@ def run_lora_step(args):
                      "traffic_source": "profiles/traffic_lora_step_w14336x4096_x8192.json (rocprofv3 "
                                        "FETCH_SIZE + WRITE_SIZE per launch, calibrated; not measured in this run)",
                      "avg_kernel_ms": round(fwd_ms, 4), "flops_per_launch": gemm_flops,
-                     "timing": "HIP events around each launch on its stream, mean over the timed steps"},
+                     "timing": f"HIP events around each launch on its stream, mean over one timed step in "
+                               f"{EV_EVERY} ({n_sampled} of {args.steps}, from the first)"},
         "bwd_dx": {"kernel": "k_gemm_bwd_rw<BF16>", "achieved": round(bwd_tf, 2), "unit": "TFLOP/s",
                    "frac": round(bwd_tf / MFMA_BF16_PEAK_TFLOPS, 4), "avg_kernel_ms": round(bwd_ms, 4)},
         "dequant": {"kernel": "k_dequantize<BF16>", "value": round(deq_gbs, 1), "unit": "GB/s",
