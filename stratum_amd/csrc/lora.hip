@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256, 2) void k_lora_pass(LoraArgs g) {
 #pragma unroll
                 for (int k = 0; k < G; ++k)
                     a[k] = *reinterpret_cast<const uint4*>(qs + (16 * k + lr) * LR_QS + 32 * mc + 8 * lh);
-#pragma unroll 1
+#pragma unroll
                 for (int f = 0; f < 4; ++f) {
                     // lane lr needs rows 32 mc + 8 lh + 0..7 of column 64 w + 16 f + lr:
                     // two transposed reads of 4 rows x 16 columns, in which lane s of
@@ -351,15 +351,18 @@ __global__ __launch_bounds__(256) void k_lora_reduce(const float* __restrict__ p
 
 int rank_padded(int R) { return R <= 16 ? 16 : 32; }
 
-// Blocks over the rows: about two work-groups per CU of MI355X's 256 in total.
-// The buffer resource of a work-group's rows spans rows_per_block * cols * 2
+// Blocks over the rows: about two work-groups per CU of MI355X's 256 in total,
+// three for the row-and-column pass at ranks up to 16 (three of those fit a CU:
+// 164 VGPRs, 43 KB of LDS; at the LoRA-step shape 512 work-groups took 58 us
+// and 768 took 53). The buffer resource of a work-group's rows spans
+// rows_per_block * cols * 2
 // bytes, which stays at most 2^31: the offset that marks a column outside the
 // matrix (2^31) must lie outside every range.
 constexpr int64_t kMaxRangeBytes = (int64_t)1 << 31;
 
-int64_t rows_per_block(int64_t rows, int64_t cols) {
+int64_t rows_per_block(int64_t rows, int64_t cols, bool three_per_cu) {
     const int64_t ncb = cols > 0 ? (cols + LR_TN - 1) / LR_TN : 1;
-    int64_t nrb = (512 + ncb - 1) / ncb;
+    int64_t nrb = ((three_per_cu ? 768 : 512) + ncb - 1) / ncb;
     const int64_t steps = (rows + LR_SM - 1) / LR_SM;
     if (nrb > steps) nrb = steps;
     if (nrb < 1) nrb = 1;
@@ -379,7 +382,7 @@ LoraPlan plan(int64_t rows, int64_t cols, int R, bool row, bool col) {
     LoraPlan p;
     const int rp = rank_padded(R);
     p.ncb = (cols + LR_TN - 1) / LR_TN;
-    p.rpb = rows_per_block(rows, cols);
+    p.rpb = rows_per_block(rows, cols, row && col && rp == 16);
     p.nrb = rows > 0 ? (rows + p.rpb - 1) / p.rpb : 0;
     p.row_bytes = row ? p.ncb * rows * rp * 4 : 0;
     p.col_bytes = col ? p.nrb * cols * rp * 4 : 0;

@@ -240,9 +240,12 @@ def test_lora_arguments_are_rejected_without_a_gpu(L):
 def test_lora_workspace_sizing(L):
     """fp32 partials: [column blocks of 256][rows][RP] for the row-direction sums
     and [row blocks][cols][RP] for the column-direction sums, RP = rank rounded
-    up to 16; about 512 work-groups (row blocks of whole 64-row steps)."""
-    # lora_dy at the 8192 x 14336 shape: 56 column blocks, 10 row blocks of 832 rows
-    assert L.stm_lora_workspace_bytes(8192, 14336, 16, 1) == 56 * 8192 * 16 * 4 + 10 * 14336 * 16 * 4
+    up to 16; about 512 work-groups (row blocks of whole 64-row steps), 768 for
+    the two-direction pass at RP = 16."""
+    # lora_dy at the 8192 x 14336 shape: 56 column blocks, 13 row blocks of 640 rows
+    assert L.stm_lora_workspace_bytes(8192, 14336, 16, 1) == 56 * 8192 * 16 * 4 + 13 * 14336 * 16 * 4
+    # rank 32 (RP = 32): two work-groups per CU, 10 row blocks of 832 rows
+    assert L.stm_lora_workspace_bytes(8192, 14336, 32, 1) == 56 * 8192 * 32 * 4 + 10 * 14336 * 32 * 4
     # lora_down / lora_da on X [8192, 4096]: 16 column blocks, 32 row blocks of 256 rows
     assert L.stm_lora_workspace_bytes(8192, 4096, 16, 0) == 16 * 8192 * 16 * 4
     assert L.stm_lora_workspace_bytes(8192, 4096, 16, 2) == 32 * 4096 * 16 * 4
