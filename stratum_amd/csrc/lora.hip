@@ -288,19 +288,36 @@ __global__ __launch_bounds__(256, 2) void k_lora_pass(LoraArgs g) {
     }
 }
 
-// out = scale * sum_p part[p][i][r] for i < items, r < R, rounded once; out is
-// [items, R] or, with TR, [R, items]. A work-group takes 64 four-rank vectors;
-// its four waves sum the blocks p = w, w + 4, ... (four loads in flight), and
-// wave 0 adds the four sums in wave order: a fixed order, so the result does not
-// depend on scheduling.
+// One reduction of a launch: out = scale * sum_p part[p][i][r] for i < items,
+// r < R, rounded once, over `grid` work-groups.
+struct RedJob {
+    const float* part;
+    int blocks;
+    int64_t items;
+    float scale;
+    uint16_t* out;
+    unsigned grid;
+};
+
+// out is [items, R] or, with TR, [R, items]. Up to two independent jobs per
+// launch (U and dB of one pass): work-groups [0, j0.grid) run j0, the rest j1.
+// A work-group takes 64 four-rank vectors; its four waves sum the blocks
+// p = w, w + 4, ... (four loads in flight), and wave 0 adds the four sums in
+// wave order: a fixed order, so the result does not depend on scheduling.
 template <typename Tr, bool TR>
-__global__ __launch_bounds__(256) void k_lora_reduce(const float* __restrict__ part, int blocks, int64_t items,
-                                                     int rank, int rp, float scale, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_lora_reduce(RedJob j0, RedJob j1, int rank, int rp) {
+    const bool second = blockIdx.x >= j0.grid;
+    const RedJob& j = second ? j1 : j0;
+    const float* __restrict__ part = j.part;
+    const int blocks = j.blocks;
+    const int64_t items = j.items;
+    const float scale = j.scale;
+    uint16_t* __restrict__ out = j.out;
     __shared__ float4 sums[4][64];
     const int per = rank / 4;
     const int64_t total = items * per;
     const int il = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t v = blockIdx.x * 64 + il;
+    const int64_t v = (int64_t)(blockIdx.x - (second ? j0.grid : 0u)) * 64 + il;
     const bool live = v < total;
     const int64_t i = live ? v / per : 0;
     const int r = live ? 4 * (int)(v - i * per) : 0;
@@ -415,18 +432,27 @@ void launch_pass(const LoraArgs& a, int dtype, bool row, bool col, dim3 grid, hi
     }
 }
 
+RedJob red_job(const float* part, int blocks, int64_t items, int R, float scale, void* out) {
+    return RedJob{part, blocks, items, scale, (uint16_t*)out, reduce_grid(items, R)};
+}
+
+// One launch for j0 and, when j1.grid > 0, j1 (both the same orientation).
+void launch_reduce(const RedJob& j0, const RedJob& j1, int R, bool tr, int dtype, hipStream_t st) {
+    const int rp = rank_padded(R);
+    const unsigned grid = j0.grid + j1.grid;
+    if (grid == 0) return;
+    if (dtype == STM_BF16) {
+        if (tr) hipLaunchKernelGGL((k_lora_reduce<BF16, true>), dim3(grid), dim3(256), 0, st, j0, j1, R, rp);
+        else hipLaunchKernelGGL((k_lora_reduce<BF16, false>), dim3(grid), dim3(256), 0, st, j0, j1, R, rp);
+    } else {
+        if (tr) hipLaunchKernelGGL((k_lora_reduce<F16, true>), dim3(grid), dim3(256), 0, st, j0, j1, R, rp);
+        else hipLaunchKernelGGL((k_lora_reduce<F16, false>), dim3(grid), dim3(256), 0, st, j0, j1, R, rp);
+    }
+}
+
 void launch_reduce(const float* part, int blocks, int64_t items, int R, float scale, void* out, bool tr, int dtype,
                    hipStream_t st) {
-    const int rp = rank_padded(R);
-    const unsigned grid = reduce_grid(items, R);
-    uint16_t* o = (uint16_t*)out;
-    if (dtype == STM_BF16) {
-        if (tr) hipLaunchKernelGGL((k_lora_reduce<BF16, true>), dim3(grid), dim3(256), 0, st, part, blocks, items, R, rp, scale, o);
-        else hipLaunchKernelGGL((k_lora_reduce<BF16, false>), dim3(grid), dim3(256), 0, st, part, blocks, items, R, rp, scale, o);
-    } else {
-        if (tr) hipLaunchKernelGGL((k_lora_reduce<F16, true>), dim3(grid), dim3(256), 0, st, part, blocks, items, R, rp, scale, o);
-        else hipLaunchKernelGGL((k_lora_reduce<F16, false>), dim3(grid), dim3(256), 0, st, part, blocks, items, R, rp, scale, o);
-    }
+    launch_reduce(red_job(part, blocks, items, R, scale, out), RedJob{}, R, tr, dtype, st);
 }
 
 int check_common(const char* what, int64_t rows, int64_t cols, int R, int dtype) {
@@ -516,8 +542,9 @@ extern "C" int stm_lora_dy(const void* dY, const void* B, const void* T, void* U
     }
     LoraArgs a{(const uint16_t*)dY, (const uint16_t*)B, (const uint16_t*)T, prow, pcol, M, N, rank, 0, (int)p.rpb};
     launch_pass(a, dtype, true, col, dim3((unsigned)p.ncb, (unsigned)p.nrb), st);
-    launch_reduce(prow, (int)p.ncb, M, rank, scaling, U, false, dtype, st);
-    if (col) launch_reduce(pcol, (int)p.nrb, N, rank, 1.f, dB, false, dtype, st);
+    // U and dB in one reduce launch
+    launch_reduce(red_job(prow, (int)p.ncb, M, rank, scaling, U),
+                  col ? red_job(pcol, (int)p.nrb, N, rank, 1.f, dB) : RedJob{}, rank, false, dtype, st);
     return check_launch("lora_dy");
 }
 
