@@ -2353,7 +2353,7 @@ struct GbCfg {
     static constexpr int kLds = kLut + 2 * kBuf;
     static_assert(kLds <= 160 * 1024, "LDS");
     static_assert(XR * PR == 512, "one dY copy per wave and group");
-    static_assert(PR <= 32 && (PR & (PR - 1)) == 0, "piece swizzle");
+    static_assert(PR >= 16 && PR <= 32 && (PR & (PR - 1)) == 0, "piece p ^ (m % 16) stays within the row");
 };
 constexpr int GB_MAX_M = 32;
 
