@@ -10,6 +10,9 @@
   host memory and streamed through NF4LayerStream with lookahead 1; every
   weight bit-exact against the oracle at its yield.
 
+* Decode-sized rows (1, 16, 32) on the full W [14336, 4096]: the small-M
+  forward and input gradient with their rank-16 LoRA terms.
+
 GEMMs are held to the whole-matrix and the per-32x32-fragment bar
 (tests/gpu_checks.py) against an fp32 matmul of the oracle-dequantized weight;
 packed codes, absmax and dequantized weights are bit-exact.
@@ -285,3 +288,26 @@ def test_lora_step_forced_fused_module_step(cuda, lora_step, monkeypatch):
     assert_gemm_close(x.grad, xr.grad, torch.bfloat16, "module dX")
     assert_gemm_close(lin.lora_A.grad, Ar.grad, torch.bfloat16, "dA")
     assert_gemm_close(lin.lora_B.grad, Br.grad, torch.bfloat16, "dB")
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+def test_decode_size_forward_and_input_gradient_at_full_weight_size(cuda, lora_step, M):
+    """Decode-sized rows on the full W [14336, 4096]: the weight-streaming
+    small-M forward (split-free up to 16 rows, ranges + reduce at 32) and
+    input gradient (ranges of weight rows + reduce), each with its rank-16
+    LoRA term at an init that makes the term as large as the base product;
+    whole matrix and every fragment against fp32 on the oracle weight."""
+    from stratum_amd.functional import nf4_gemm_bwd_dx, nf4_gemm_fwd
+    _, N, K, R = LORA_STEP
+    s = lora_step
+    x, dy = s["x"][:M].contiguous(), s["dy"][:M].contiguous()
+    A = seeded((R, K), 20, 0.1, torch.bfloat16).to(cuda)
+    B = seeded((N, R), 21, 0.1, torch.bfloat16).to(cuda)
+    t = (x.float() @ A.float().t().contiguous()).to(torch.bfloat16)
+    u = (dy.float() @ B.float()).to(torch.bfloat16)
+    y = nf4_gemm_fwd(x, s["q"], s["a"], (N, K), 64, lora_t=t, lora_b=B)
+    ref = x.float() @ s["w"].t().contiguous() + t.float() @ B.float().t().contiguous()
+    assert_gemm_close(y, ref, torch.bfloat16, f"M = {M} forward with LoRA")
+    dx = nf4_gemm_bwd_dx(dy, s["q"], s["a"], (N, K), 64, lora_u=u, lora_at=A.t().contiguous())
+    ref = dy.float() @ s["w"] + u.float() @ A.float()
+    assert_gemm_close(dx, ref, torch.bfloat16, f"M = {M} input gradient with U . A")
