@@ -183,6 +183,8 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
     (24, 4160, 320, 64, 16),           # 32-row variant: last group 64 rows, LoRA in the reduce
     (32, 14336, 1024, 128, 0),         # 32-row variant at its row limit, blocksize 128
     (20, 448, 768, 256, 16),           # 32-row variant: groups of 128 and 64 rows, blocksize 256
+    (7, 2048, 512, 64, 32),            # small-M input gradient, rank 32 in the reduce
+    (29, 1024, 1024, 128, 64),         # 32-row variant, rank 64 in the reduce
 ])
 def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
     from stratum_amd import _lib
