@@ -148,7 +148,7 @@ int stm_nf4_gemm_fwd_noalloc(const void* X, const uint8_t* packed, const float* 
  * torch.autograd.backward at stratum/runtime.py:340-341. The optional rank-R term
  * is the LoRA input gradient (U = scale * dY . B, At = A^T).
  *   workspace    : as stm_nf4_gemm_fwd, sized by stm_nf4_gemm_workspace_bytes(M, N, K, 1).
- *                  At most 32 rows run a weight-streaming kernel when this
+ *                  At most 64 rows run a weight-streaming kernel when this
  *                  workspace is given (its ranges of weight rows write fp32
  *                  partials that a second kernel sums with the LoRA term);
  *                  without it the tile kernels run (2-3x slower there).

@@ -2312,10 +2312,10 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
 }
 
 // ----------------------------------------------------- small-M input gradient
-// dX[M, K] = dY[M, N] . W[N, K] for M <= 32 rows, bound by dequantizing the
+// dX[M, K] = dY[M, N] . W[N, K] for M <= 64 rows, bound by dequantizing the
 // streamed weight. A work-group owns 256 output columns k (128 bytes of every
 // packed weight row) and one range of weight rows n (the reduction), walked in
-// groups of GN rows (256, or 128 for 17..32 rows, whose doubled dY buffers
+// groups of GN rows (256, or 128 above 16 rows, whose larger dY buffers
 // must fit); each range writes fp32 partials [split][m][k] that k_split_reduce
 // sums (adding the LoRA term U . At^T). Wave w owns the columns [32 w, 32 w + 32)
 // of the block: two 16-column tiles of v_mfma_f32_16x16x32 (weight side: 16
@@ -2343,6 +2343,7 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
 template <int MB>
 struct GbCfg {
     static constexpr int KW = 256, GN = MB == 1 ? 256 : 128, XR = 16 * MB;
+    static constexpr int XC = XR * (GN / 8) / 512;  // dY copies per wave and group
     static constexpr int NSUB = GN / 64;   // 64-row subgroups per group
     static constexpr int PR = GN / 8;      // 16-byte dY pieces per row and group
     static constexpr int kLut = 256 * RW_LUT_COPIES * 8;
@@ -2352,10 +2353,10 @@ struct GbCfg {
     static constexpr int kBuf = kW + kA + kX;
     static constexpr int kLds = kLut + 2 * kBuf;
     static_assert(kLds <= 160 * 1024, "LDS");
-    static_assert(XR * PR == 512, "one dY copy per wave and group");
+    static_assert(XR * PR == 512 * XC && XC >= 1, "whole dY copies per wave and group");
     static_assert(PR >= 16 && PR <= 32 && (PR & (PR - 1)) == 0, "piece p ^ (m % 16) stays within the row");
 };
-constexpr int GB_MAX_M = 32;
+constexpr int GB_MAX_M = 64;
 
 template <typename Tr, int MB>
 __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_split) {
@@ -2401,12 +2402,17 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
         const int64_t cb = k0 / 2 + 16 * ((lane & 7) ^ swz_key(wrow[j]));
         wcol[j] = cb + 16 <= K / 2 ? cb : K / 2 - 16;
     }
-    // dY copies: wave w copies rows (64 / PR) w + 0.. when they exist; the lane
-    // fills slot lane % PR of row (64 / PR) w + lane / PR, piece (lane % PR) ^ (row % 16)
-    const int xm = (64 / PR) * wave + lane / PR;
-    const bool xon = xm < M;
-    const int xp = (lane % PR) ^ (xm & 15);
-    const uint16_t* xsrc = dy + (xon ? xm : 0) * N + 8 * xp;
+    // dY copies: copy j of wave w fills slots 512 j + 64 w + lane of the XR x PR
+    // slots, i.e. slot lane % PR of row (512 j + 64 w + lane) / PR, piece
+    // (lane % PR) ^ (row % 16), when the row exists
+    int xm[C::XC], xp[C::XC];
+    const uint16_t* xsrc[C::XC];
+#pragma unroll
+    for (int j = 0; j < C::XC; ++j) {
+        xm[j] = (512 * j + 64 * wave + lane) / PR;
+        xp[j] = (lane % PR) ^ (xm[j] & 15);
+        xsrc[j] = dy + (xm[j] < M ? xm[j] : 0) * N + 8 * xp[j];
+    }
 
     auto copy_group = [&](int grp, int b) {
         const int64_t n0 = (int64_t)grp * GN;
@@ -2428,7 +2434,10 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
                      uniform((uint32_t)(size_t)((const __attribute__((address_space(3))) float*)(ba(b) + 64 * i))));
             }
         }
-        if (xon) dma16(xsrc + (n0 + 8 * xp < N ? n0 : -8 * xp), uniform(lds_offset(bx(b) + 64 * wave)));
+#pragma unroll
+        for (int j = 0; j < C::XC; ++j)
+            if (xm[j] < M)
+                dma16(xsrc[j] + (n0 + 8 * xp[j] < N ? n0 : -8 * xp[j]), uniform(lds_offset(bx(b) + 512 * j + 64 * wave)));
     };
 
     const int c = lane & 15, gq = lane >> 4;
@@ -2989,7 +2998,7 @@ bool use_gemv_bwd(int64_t M, int64_t N, int64_t K, int num_groups) {
 // above 16 rows) that minimise rounds x (fixed cost + groups per range) over the
 // 256-column work-groups; returns the range count and sets the groups per range.
 int gemv_bwd_splits(int64_t M, int64_t N, int64_t K, int* groups_per_split) {
-    const int64_t gn = M <= 16 ? GbCfg<1>::GN : GbCfg<2>::GN;
+    const int64_t gn = M <= 16 ? GbCfg<1>::GN : M <= 32 ? GbCfg<2>::GN : GbCfg<4>::GN;
     const int64_t blocks = (K + GbCfg<1>::KW - 1) / GbCfg<1>::KW, groups = (N + gn - 1) / gn;
     int64_t best_gps = groups > 0 ? groups : 1;
     double best_t = 1e30;
@@ -3114,17 +3123,19 @@ int launch_gemv_bwd(GemmArgs g, int dtype, hipStream_t stream) {
     g.splits = gemv_bwd_splits(g.M, g.N, g.K, &gps);
     const int64_t tiles = (g.K + GbCfg<1>::KW - 1) / GbCfg<1>::KW * g.splits;  // k_gemv_bwd deals them per XCD
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8)), block(512);
+#define STM_GB_LAUNCH(MB)                                                              \
+    if (dtype == STM_BF16)                                                             \
+        hipLaunchKernelGGL((k_gemv_bwd<BF16, MB>), grid, block, 0, stream, g, gps);   \
+    else                                                                               \
+        hipLaunchKernelGGL((k_gemv_bwd<F16, MB>), grid, block, 0, stream, g, gps);
     if (g.M <= 16) {
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_bwd<BF16, 1>), grid, block, 0, stream, g, gps);
-        else
-            hipLaunchKernelGGL((k_gemv_bwd<F16, 1>), grid, block, 0, stream, g, gps);
+        STM_GB_LAUNCH(1)
+    } else if (g.M <= 32) {
+        STM_GB_LAUNCH(2)
     } else {
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_bwd<BF16, 2>), grid, block, 0, stream, g, gps);
-        else
-            hipLaunchKernelGGL((k_gemv_bwd<F16, 2>), grid, block, 0, stream, g, gps);
+        STM_GB_LAUNCH(4)
     }
+#undef STM_GB_LAUNCH
     const int rc = check_launch("gemm_bwd_dx (small M)");
     if (rc != STM_OK) return rc;
     return launch_split_reduce(g, g.K, nullptr, dtype, stream, true);

@@ -185,6 +185,10 @@ def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank)
     (20, 448, 768, 256, 16),           # 32-row variant: groups of 128 and 64 rows, blocksize 256
     (7, 2048, 512, 64, 32),            # small-M input gradient, rank 32 in the reduce
     (29, 1024, 1024, 128, 64),         # 32-row variant, rank 64 in the reduce
+    (33, 64, 64, 64, 0),               # 64-row variant (two dY copies per wave): one subgroup
+    (48, 4160, 320, 64, 16),           # 64-row variant: last group 64 rows, LoRA in the reduce
+    (64, 14336, 1024, 128, 0),         # 64-row variant at its row limit, blocksize 128
+    (57, 448, 768, 256, 32),           # 64-row variant: groups of 128 and 64 rows, blocksize 256, rank 32
 ])
 def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank):
     from stratum_amd import _lib
