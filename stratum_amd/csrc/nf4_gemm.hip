@@ -3029,6 +3029,14 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
 #ifndef STM_FWD_R8_AUTO
 #define STM_FWD_R8_AUTO 1
 #endif
+// Longest reduction the automatic choice runs on the 8-wave forward. Measured
+// (auto plans, same box, µs, 4-wave against 8-wave): K = 4096 and 14336 at
+// M = 1024-4096: 116.3 / 118.3, 224.5 / 230.6, 442.5 / 458.2 ([14336,4096]),
+// 410.2 / 431.0 ([4096,14336] at M = 4096), 126.2 / 130.2 ([4096,4096]); at
+// K = 1024-2048 the 8-wave kernel is 1-7 % faster (shorter per-item fixed cost).
+#ifndef STM_FWD_R8_MAX_K
+#define STM_FWD_R8_MAX_K 2048
+#endif
 
 // 1: small-M forwards that fit k_gemv_ks run it (no split reduction).
 #ifndef STM_GEMV_KS
@@ -3098,11 +3106,12 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;
     const bool rw = STM_FWD_RW && rw_split_ok(false, g.splits, g.K / BK) && rw_offsets_fit(g);
     int rc;
-    // unsplit single-matrix 256 x 256 tiles up to 4096 rows run the 8-wave
-    // kernel (3-7 % faster at M = 2048-4096 with N = 3072-6144; 1-2 % slower at
-    // M = 8192, which keeps the 4-wave kernel); pinned kinds keep their kernel
+    // unsplit single-matrix 256 x 256 tiles up to 4096 rows and reductions up to
+    // STM_FWD_R8_MAX_K run the 8-wave kernel (1-7 % faster at K = 1024-2048;
+    // slower at M = 8192 and on longer reductions, which keep the 4-wave
+    // kernel); pinned kinds keep their kernel
     const bool auto_r8 = STM_FWD_R8_AUTO && p.kind == kBig && tile_override() < 0 && g.num_groups == 1 &&
-                         g.splits == 1 && g.M <= 4096;
+                         g.splits == 1 && g.M <= 4096 && g.K <= STM_FWD_R8_MAX_K;
     if (p.kind == kBig && g.group_bm == 192 && g.num_groups > 1 && g.splits == 1 && rw && tile_override() < 0)
         rc = launch_fwd_rw<192, 1>(g, dtype, stream);
     else if ((p.kind == kBig8 || auto_r8) && rw_offsets_fit(g))
