@@ -2876,6 +2876,16 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
 #ifndef STM_T_MID_FWD
 #define STM_T_MID_FWD 1.55  // per step with every CU busy (1.2-1.3 on a half-empty GPU)
 #endif
+// The forward's per-step time when its 128 x 256 tiles fill less than one
+// round of the CUs. Measured with it on the shapes whose plan it flips from
+// the split 256 x 256 tile to the unsplit 128 x 256 tile, µs before -> after:
+// W [14336,4096] at M = 320 / 384 / 448: 87.9 / 85.0 / 86.0 -> 74.3 / 70.7 /
+// 74.0; [8192,4096] at M = 640 / 768: 79.1 / 81.8 -> 69.6 / 70.5; [4096,4096]
+// at M = 1408 / 1536: 80.2 / 81.5 -> 69.3 / 70.3; [5632,2048] at M = 704:
+// 45.4 -> 39.0; [2048,5632] at M = 3072: 101.7 -> 93.2.
+#ifndef STM_T_MID_FWD_PART
+#define STM_T_MID_FWD_PART 1.25
+#endif
 #ifndef STM_T_MID_BWD
 #define STM_T_MID_BWD 1.1
 #endif
@@ -2916,7 +2926,9 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     // big tiles run the register-weight kernels when unsplit, and for the input
     // gradient also when split into ranges of >= 32 steps (rw_split_ok)
     const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2, t_small = backward ? 1.35 : 0.8;
-    const double t_mid = backward ? STM_T_MID_BWD : STM_T_MID_FWD;
+    // (the input gradient's 128 x 256 tile gains nothing comparable on a part of
+    // the CUs: the same change there measured -14 .. +9 % by shape)
+    const double t_mid = backward ? STM_T_MID_BWD : (mid_tiles < kCUs ? STM_T_MID_FWD_PART : STM_T_MID_FWD);
     int max_sp = 1;
     if (num_groups == 1) {
         const int64_t by_steps = steps / 8;
