@@ -2889,6 +2889,9 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
 #ifndef STM_T_MID_BWD
 #define STM_T_MID_BWD 1.1
 #endif
+#ifndef STM_BWD_MID_MAX_STEPS
+#define STM_BWD_MID_MAX_STEPS 48
+#endif
 
 // Whether a 256 x 256 launch of `splits` ranges over `steps` reduction steps runs
 // the register-weight kernel. Measured on MI355X: unsplit always wins; split, the
@@ -2935,6 +2938,16 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
         max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
     }
     const int only = tile_override();
+    // Input gradient: the unsplit 128 x 256 tile when its tiles fill 1/4 to one
+    // round of the CUs and the reduction is at most 48 steps (weights of up to
+    // 3072 rows). The cost model favours split 256 x 256 launches there, which
+    // measured slower, µs: W [2048,1024] at M = 2048 41.3 -> 35.6, [2048,2048]
+    // at M = 1024 41.5 -> 35.8, [3072,1024] at M = 2048 50.2 -> 49.1, the other
+    // such shapes within 1 %. At 88-96 steps the same rule measured -7 .. +43 %
+    // ([5632,2048], [6144,1024], [6144,4096]), so longer reductions keep the model.
+    if (STM_MID_TILE && backward && only < 0 && num_groups == 1 && mid_tiles >= kCUs / 4 && mid_tiles <= kCUs &&
+        steps <= STM_BWD_MID_MAX_STEPS)
+        return Plan{kMid, mid_tiles, 1};
     Plan best{only < 0 ? (int)kBig : only, only == kSmall ? small_tiles : only == kMid ? mid_tiles : big_tiles, 1};
     double best_t = 1e300;
     for (int sp = 1; sp <= max_sp; ++sp) {
