@@ -2889,6 +2889,19 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
 #ifndef STM_T_MID_BWD
 #define STM_T_MID_BWD 1.1
 #endif
+// Forward planner calibration, re-measured with the current kernels (auto
+// plans, µs before -> after): the 128 x 128 tile's per-step time is 0.95 µs
+// (0.8 before) and forward splits stop at 8 ranges (16 before: the model's
+// 16-range plans measured slower). W [4096,4096] at M = 640: 58.1 -> 51.1;
+// [6144,4096] at M = 384 / 512: 57.7 / 57.2 -> 50.7 / 54.1; [3072,4096] at
+// M = 768 / 1024: 57.0 / 57.1 -> 48.1 / 54.2; K = 1024 shapes 2-5 % faster;
+// no measured shape slower (19 shapes, M = 64-1024).
+#ifndef STM_FWD_MAX_SPLIT
+#define STM_FWD_MAX_SPLIT 8
+#endif
+#ifndef STM_T_SMALL_FWD
+#define STM_T_SMALL_FWD 0.95
+#endif
 #ifndef STM_BWD_MID_MAX_STEPS
 #define STM_BWD_MID_MAX_STEPS 48
 #endif
@@ -2928,7 +2941,8 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     const int64_t steps = red / BK;
     // big tiles run the register-weight kernels when unsplit, and for the input
     // gradient also when split into ranges of >= 32 steps (rw_split_ok)
-    const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2, t_small = backward ? 1.35 : 0.8;
+    const double t_big_rw = backward ? 1.85 : 2.0, t_big = backward ? 2.45 : 2.2,
+                 t_small = backward ? 1.35 : STM_T_SMALL_FWD;
     // (the input gradient's 128 x 256 tile gains nothing comparable on a part of
     // the CUs: the same change there measured -14 .. +9 % by shape)
     const double t_mid = backward ? STM_T_MID_BWD : (mid_tiles < kCUs ? STM_T_MID_FWD_PART : STM_T_MID_FWD);
@@ -2936,6 +2950,7 @@ Plan plan(int64_t M, int64_t cols, int64_t red, bool backward, int num_groups) {
     if (num_groups == 1) {
         const int64_t by_steps = steps / 8;
         max_sp = (int)(by_steps < 16 ? (by_steps > 1 ? by_steps : 1) : 16);
+        if (!backward && max_sp > STM_FWD_MAX_SPLIT) max_sp = STM_FWD_MAX_SPLIT;
     }
     const int only = tile_override();
     // Input gradient: the unsplit 128 x 256 tile when its tiles fill 1/4 to one
