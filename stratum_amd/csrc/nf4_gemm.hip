@@ -2908,12 +2908,20 @@ double plan_cost(int64_t tiles, int64_t steps, int sp, double t_step, int64_t M,
 
 // Whether a 256 x 256 launch of `splits` ranges over `steps` reduction steps runs
 // the register-weight kernel. Measured on MI355X: unsplit always wins; split, the
-// input gradient wins with at most 4 ranges of >= 32 steps (-14..-22 % at
-// M = 512..2048) and loses with more, shorter ranges (+11..+41 % at 7..16 ranges
-// of 14..32 steps); the split forward loses (+4..+20 %).
+// input gradient wins with at most 4 ranges of at least STM_RW_SPLIT_MIN_STEPS
+// steps and loses with more, shorter ranges (+11..+41 % at 7..16 ranges of
+// 14..32 steps); the split forward loses (+4..+20 %).
+// Shortest range a split input gradient gives the register-weight kernel
+// (shorter ranges take the LDS-weight kernel). Re-measured with the current
+// kernels, auto plans, µs 32 -> 64: W [14336,4096] at M = 768 / 1024 142.5 /
+// 171.5 -> 122.3 / 140.3; [6144,4096] at M = 1024 110.2 -> 85.9; [11008,4096]
+// at M = 768 / 1024 123.6 / 152.6 -> 102.4 / 124.4; 14 other shapes unchanged.
+#ifndef STM_RW_SPLIT_MIN_STEPS
+#define STM_RW_SPLIT_MIN_STEPS 64
+#endif
 bool rw_split_ok(bool backward, int splits, int64_t steps) {
     if (splits <= 1) return true;
-    return backward && splits <= 4 && (steps + splits - 1) / splits >= 32;
+    return backward && splits <= 4 && (steps + splits - 1) / splits >= STM_RW_SPLIT_MIN_STEPS;
 }
 
 // Tile restriction: -1 = cost model, else one TileKind (tests use it to reach
