@@ -1828,39 +1828,45 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 }
 
 // ------------------------------------------------------------ small-M forward
-// Y[M, N] = X[M, K] . W[N, K]^T for M <= 32 rows (decode-sized batches),
+// Y[M, N] = X[M, K] . W[N, K]^T for M <= 64 rows (decode-sized batches),
 // bound by dequantizing the streamed weight. A work-group owns 32 weight rows
 // per wave (two v_mfma_f32_16x16x32 tiles of weight rows x activation rows,
 // 16 MB activation rows; GvCfg) over one reduction range, walked in groups of
-// 256. Every operand
-// reaches LDS through lane-contiguous global -> LDS copies (whole cache lines,
-// one L1 access per line), double-buffered, one barrier per group:
-//  - packed weight: each wave copies its own 32 rows x 128 bytes (8 lanes per
-//    row); the 16-byte piece p of row r sits in slot p ^ ((r >> 1) & 7), so
-//    the MFMA-layout reads (16 lanes = 16 rows, same piece) hit all banks once;
+// GK = 256 (128 above 32 rows, whose larger activation buffers must fit).
+// Every operand reaches LDS through lane-contiguous global -> LDS copies
+// (whole 64- or 128-byte row pieces), double-buffered, one barrier per group:
+//  - packed weight: each wave copies its own 32 rows x GK / 2 bytes (PW
+//    16-byte pieces per row); piece p of row r sits in slot
+//    p ^ ((r >> WSH) % PW), so the MFMA-layout reads (16 lanes = 16 rows,
+//    same piece) hit all banks once;
 //  - absmax: each wave copies its rows' blocks of the group (dword copies);
-//  - activations: the group's <= 16 MB rows x 512 bytes, shared by the waves,
-//    piece p of row m in slot p ^ (m % 16).
-// Within a group, 128-deep chunk c (0, 1): lane (r = lane % 16, h = lane / 16)
+//  - activations: the group's <= 16 MB rows x 2 GK bytes, shared by the
+//    waves, piece p of row m in slot p ^ (m % 16).
+// Within a group, 128-deep chunk c: lane (r = lane % 16, h = lane / 16)
 // reads 16 packed bytes (k = 128 c + 32 h + 0..31) of row r of each tile and
 // their absmax, dequantizes in registers with the level table as in
 // k_gemm_fwd_rw, and MFMA q (0..3) takes k = 128 c + 32 h + 8 q + (0..7) from
-// both operands. Past K (K % 256 != 0) the copies read valid addresses and
+// both operands. Past K (K % GK != 0) the copies read valid addresses and
 // the lanes use a zero scale and zero activations. Reduction ranges (splits)
 // write fp32 partials [split][m][n] that k_split_reduce sums (with bias and
 // the LoRA term); with one range the output (plus bias) is stored directly.
-// Work-group shape of the small-M forward for up to 16 MB activation rows:
-// WAVES waves of 32 weight rows (two 16-row MFMA tiles) each. MB = 1: 8 waves
-// (256 rows); MB = 2: 6 waves (192 rows), so the doubled activation buffers
-// still fit beside the 64 KB level table (150 KB of LDS).
+// Work-group shape: WAVES waves of 32 weight rows (two 16-row MFMA tiles)
+// each. MB = 1: 8 waves (256 rows); MB = 2: 6 waves (192 rows), so the
+// doubled activation buffers still fit beside the 64 KB level table (150 KB
+// of LDS); MB = 4: 8 waves over groups of 128 (132 KB).
 template <int MB>
 struct GvCfg {
-    static constexpr int WAVES = MB == 1 ? 8 : 6, R = 2, RW = 32, ROWS = RW * WAVES, XR = 16 * MB, GK = 256;
-    static constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = XR * 32 * 16, kW = ROWS * 8 * 16, kA = ROWS * 4 * 4;
+    static constexpr int WAVES = MB == 2 ? 6 : 8, R = 2, RW = 32, ROWS = RW * WAVES, XR = 16 * MB;
+    static constexpr int GK = MB == 4 ? 128 : 256;       // reduction depth of a group
+    static constexpr int PW = GK / 32, PX = GK / 8;      // 16-byte pieces of a weight row, an activation row
+    static constexpr int NCH = GK / 128, NFL = GK / 64;  // 128-deep chunks; absmax per row (blocksize >= 64)
+    static constexpr int WSH = PW == 8 ? 1 : 2;          // weight slot swizzle: piece ^ ((row >> WSH) % PW)
+    static constexpr int kLut = 256 * RW_LUT_COPIES * 8, kX = XR * PX * 16, kW = ROWS * PW * 16, kA = ROWS * NFL * 4;
     static constexpr int kLds = kLut + 2 * (kX + kW + kA);
     static_assert(kLds <= 160 * 1024, "LDS");
+    static_assert((PW << WSH) == 16 && RW * PW % 64 == 0 && XR * PX % 64 == 0, "copy shapes");
 };
-constexpr int GV_GK = 256;
+constexpr int GV_GK = 256;  // group depth of k_gemv_ks
 
 template <typename Tr, int MB>
 __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
@@ -1874,29 +1880,32 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
     float2* lut_all = reinterpret_cast<float2*>(smem);
     auto sx = [&](int buf) { return reinterpret_cast<uint4*>(smem + C::kLut + buf * C::kX); };
     auto sw = [&](int buf) {
-        return reinterpret_cast<uint4*>(smem + C::kLut + 2 * C::kX + buf * C::kW) + wave * (C::RW * 8);
+        return reinterpret_cast<uint4*>(smem + C::kLut + 2 * C::kX + buf * C::kW) + wave * (C::RW * C::PW);
     };
     auto sa = [&](int buf) {
-        return reinterpret_cast<float*>(smem + C::kLut + 2 * (C::kX + C::kW) + buf * C::kA) + wave * (C::RW * 4);
+        return reinterpret_cast<float*>(smem + C::kLut + 2 * (C::kX + C::kW) + buf * C::kA) + wave * (C::RW * C::NFL);
     };
 
     const int64_t K = g.K, N = g.N, M = g.M;
     const int bshift = 31 - __builtin_clz(g.blocksize);
-    const int nfl = (GV_GK >> bshift) > 0 ? (GV_GK >> bshift) : 1;  // absmax per row per group
+    const int nfl = (C::GK >> bshift) > 0 ? (C::GK >> bshift) : 1;  // absmax per row per group
     const int64_t kblocks = K >> bshift;
-    const int ngroups = (int)((K + GV_GK - 1) / GV_GK);
+    const int ngroups = (int)((K + C::GK - 1) / C::GK);
     const int z = blockIdx.y;
     const int g_begin = z * groups_per_split;
     const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
     const int64_t nw0 = (int64_t)blockIdx.x * C::ROWS + wave * C::RW;  // this wave's first weight row
 
-    // copy sources (per lane; group offsets added per copy)
-    const uint8_t* wsrc[2 * R];
+    // copy sources (per lane; group offsets added per copy): weight copy i
+    // covers rows 64 / PW i + lane / PW, slot lane % PW of each
+    constexpr int PW = C::PW, WC = C::RW * PW / 64;
+    auto wslot_piece = [](int row, int slot) { return slot ^ ((row >> C::WSH) & (PW - 1)); };
+    const uint8_t* wsrc[WC];
 #pragma unroll
-    for (int i = 0; i < 2 * R; ++i) {
-        const int row = 8 * i + (lane >> 3);
+    for (int i = 0; i < WC; ++i) {
+        const int row = 64 / PW * i + lane / PW;
         const int64_t n = nw0 + row < N ? nw0 + row : N - 1;
-        wsrc[i] = g.packed + n * (K / 2) + 16 * ((lane & 7) ^ ((row >> 1) & 7));
+        wsrc[i] = g.packed + n * (K / 2) + 16 * wslot_piece(row, lane % PW);
     }
     const int a_rows_per_copy = 64 / nfl, a_copies = (C::RW * nfl + 63) / 64;  // <= R
     const float* asrc[R];
@@ -1906,24 +1915,24 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
         asrc[i] = g.absmax + (n0 < N ? n0 : N - 1) * kblocks;
     }
     const int aj = lane % nfl;
-    // activations: XR / 2 copies of two rows each, copy ix by wave ix % WAVES
-    constexpr int XI = C::XR / 2, XC = (XI + WAVES - 1) / WAVES;
+    // activations: XR PX / 64 copies of 64 / PX rows each, copy ix by wave ix % WAVES
+    constexpr int PX = C::PX, XI = C::XR * PX / 64, XC = (XI + WAVES - 1) / WAVES;
     const uint16_t* xsrc[XC];
     int xpiece[XC];
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
-        const int xm = 2 * (wave + j * WAVES) + (lane >> 5);  // activation row this lane copies
+        const int xm = 64 / PX * (wave + j * WAVES) + lane / PX;  // activation row this lane copies
         xsrc[j] = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
-        xpiece[j] = (lane & 31) ^ (xm & 15);
+        xpiece[j] = (lane % PX) ^ (xm & 15);
     }
 
     auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
     auto copy_group = [&](int grp, int buf) {
-        const int64_t kg = (int64_t)grp * GV_GK;
+        const int64_t kg = (int64_t)grp * C::GK;
 #pragma unroll
-        for (int i = 0; i < 2 * R; ++i) {
-            // bytes past the row (K % 256 != 0) read the row start instead
-            const int piece = (lane & 7) ^ (((8 * i + (lane >> 3)) >> 1) & 7);
+        for (int i = 0; i < WC; ++i) {
+            // bytes past the row (K % GK != 0) read the row start instead
+            const int piece = wslot_piece(64 / PW * i + lane / PW, lane % PW);
             const uint8_t* src = kg / 2 + 16 * piece < K / 2 ? wsrc[i] + kg / 2 : wsrc[i] - 16 * piece;
             dma16(src, uniform(lds_offset(sw(buf) + i * 64)));
         }
@@ -1938,7 +1947,7 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
         for (int j = 0; j < XC; ++j)
             if (wave + j * WAVES < XI) {
                 const int64_t k = kg + 8 * xpiece[j];
-                dma16(xsrc[j] + (k < K ? k : 0), uniform(lds_offset(sx(buf) + 2 * (wave + j * WAVES) * 32)));
+                dma16(xsrc[j] + (k < K ? k : 0), uniform(lds_offset(sx(buf) + (wave + j * WAVES) * 64)));
             }
     };
 
@@ -1956,24 +1965,24 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
     // the scale of lanes whose k is past K.
     auto compute = [&](int buf, int grp, auto tail_c) {
         constexpr bool TAIL = decltype(tail_c)::value;
-        uint4 xv[2][MB][4], qv[2 * R];
-        float av[2 * R];
+        uint4 xv[C::NCH][MB][4], qv[C::NCH * R];
+        float av[C::NCH * R];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const bool ok = !TAIL || (int64_t)grp * GV_GK + 128 * c + 32 * h < K;
+        for (int c = 0; c < C::NCH; ++c) {
+            const bool ok = !TAIL || (int64_t)grp * C::GK + 128 * c + 32 * h < K;
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int xr = 16 * mb + r;
-                    const uint4 v = sx(buf)[xr * 32 + ((16 * c + 4 * h + q) ^ r)];
+                    const uint4 v = sx(buf)[xr * PX + ((16 * c + 4 * h + q) ^ r)];
                     xv[c][mb][q] = ok ? v : make_uint4(0, 0, 0, 0);
                 }
             const int blk = (128 * c + 32 * h) >> bshift;
 #pragma unroll
             for (int t = 0; t < R; ++t) {
                 const int row = 16 * t + r;
-                qv[R * c + t] = sw(buf)[row * 8 + ((4 * c + h) ^ ((row >> 1) & 7))];
+                qv[R * c + t] = sw(buf)[row * PW + wslot_piece(row, 4 * c + h)];
                 const float a = sa(buf)[row * nfl + blk];
                 av[R * c + t] = ok ? a : 0.0f;
             }
@@ -1992,8 +2001,8 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
         };
         issue(0, p[0]);
 #pragma unroll
-        for (int i = 0; i < 2 * R; ++i) {
-            if (i + 1 < 2 * R) issue(i + 1, p[(i + 1) & 1]);
+        for (int i = 0; i < C::NCH * R; ++i) {
+            if (i + 1 < C::NCH * R) issue(i + 1, p[(i + 1) & 1]);
             sched_fence();
             const int c = i / R, t = i % R;
             const float a = av[i];
@@ -2019,7 +2028,7 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
     for (int grp = g_begin; grp < g_end; ++grp) {
         const int buf = (grp - g_begin) & 1;
         if (grp + 1 < g_end) copy_group(grp + 1, buf ^ 1);
-        if ((int64_t)(grp + 1) * GV_GK > K)
+        if ((int64_t)(grp + 1) * C::GK > K)
             compute(buf, grp, std::true_type());
         else
             compute(buf, grp, std::false_type());
@@ -2647,27 +2656,39 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
 
 
 #ifndef STM_GEMV_MAX_M
-#define STM_GEMV_MAX_M 32
+#define STM_GEMV_MAX_M 64
 #endif
 
 #ifndef STM_GEMV_T_LAT
 #define STM_GEMV_T_LAT 3.0  // fixed cost of a work-group (copy latency, level table), in groups
 #endif
-int gemv_rows_per_block(int64_t M) { return M <= 16 ? GvCfg<1>::ROWS : GvCfg<2>::ROWS; }
 
-// Small-M forward: reduction ranges (in groups of 256) that minimise
-// rounds x (fixed cost + groups per range), one work-group per CU, plus the
-// split reduce when there is more than one range.
+int gemv_rows_per_block(int64_t M) {
+    return M <= 16 ? GvCfg<1>::ROWS : M <= 32 ? GvCfg<2>::ROWS : GvCfg<4>::ROWS;
+}
+int gemv_group_depth(int64_t M) { return M <= 16 ? GvCfg<1>::GK : M <= 32 ? GvCfg<2>::GK : GvCfg<4>::GK; }
+
+// Small-M forward: reduction ranges (in groups of 256, 128 above 32 rows)
+// that minimise the estimated time, one work-group per CU, plus the split
+// reduce when there is more than one range. Up to 32 rows: rounds x (fixed
+// cost + groups per range) + 6 groups for the reduce. Above 32 rows, a fit
+// to forced range counts over eleven weight shapes (N, K from 1024 to 28672)
+// at M = 33, 48 and 64, in µs (3 % rms): 0.86 per round + 1.61 per group of
+// 128 and round, and with a split 2.87 + 0.38 per MB of partials + 0.08 per
+// range (the groups are latency-bound: one in flight per work-group).
 int gemv_splits(int64_t M, int64_t N, int64_t K) {
-    const int64_t rows = gemv_rows_per_block(M);
-    const int64_t blocks = (N + rows - 1) / rows, groups = (K + GV_GK - 1) / GV_GK;
+    const int64_t rows = gemv_rows_per_block(M), gk = gemv_group_depth(M);
+    const int64_t blocks = (N + rows - 1) / rows, groups = (K + gk - 1) / gk;
     if (groups <= 1) return 1;
     int best = 1;
     double best_t = 1e30;
     for (int64_t sp = 1; sp <= groups && sp <= 64; ++sp) {
         const int64_t gps = (groups + sp - 1) / sp, spe = (groups + gps - 1) / gps;
         const int64_t rounds = (blocks * spe + 255) / 256;
-        const double t = (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0);
+        const double t =
+            gk == 256 ? (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0)
+                      : (double)rounds * (0.86 + 1.61 * (double)gps) +
+                            (spe > 1 ? 2.87 + 0.38e-6 * (double)(spe * M * N * 4) + 0.077 * (double)spe : 0.0);
         if (t < best_t - 1e-9) best_t = t, best = (int)spe;
     }
     return best;
@@ -2676,7 +2697,8 @@ int gemv_splits(int64_t M, int64_t N, int64_t K) {
 bool use_gemv(int64_t M, int num_groups) { return num_groups == 1 && M > 0 && M <= STM_GEMV_MAX_M; }
 
 int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
-    const int ngroups = (int)((g.K + GV_GK - 1) / GV_GK);
+    const int gk = gemv_group_depth(g.M);
+    const int ngroups = (int)((g.K + gk - 1) / gk);
     const int gps = (ngroups + g.splits - 1) / g.splits;
     const int splits = gps ? (ngroups + gps - 1) / gps : 1;  // every range non-empty (K = 0: one empty range)
     g.splits = splits;
@@ -2688,12 +2710,18 @@ int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
             hipLaunchKernelGGL((k_gemv_fwd<BF16, 1>), grid, block, 0, stream, g, gps);
         else
             hipLaunchKernelGGL((k_gemv_fwd<F16, 1>), grid, block, 0, stream, g, gps);
-    } else {
+    } else if (g.M <= 32) {
         dim3 block(64 * GvCfg<2>::WAVES);
         if (dtype == STM_BF16)
             hipLaunchKernelGGL((k_gemv_fwd<BF16, 2>), grid, block, 0, stream, g, gps);
         else
             hipLaunchKernelGGL((k_gemv_fwd<F16, 2>), grid, block, 0, stream, g, gps);
+    } else {
+        dim3 block(64 * GvCfg<4>::WAVES);
+        if (dtype == STM_BF16)
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, 4>), grid, block, 0, stream, g, gps);
+        else
+            hipLaunchKernelGGL((k_gemv_fwd<F16, 4>), grid, block, 0, stream, g, gps);
     }
     int rc = check_launch("gemm_fwd (small M)");
     if (rc != STM_OK || g.splits == 1) return rc;

@@ -167,10 +167,12 @@ def test_gemm_workspace_sizing(L):
     # large problems fill the GPU with output tiles: no split, no workspace
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(8192, 14336, 4096, 1) == 0
-    # M = 33, W [14336, 4096]: the forward's 112 tiles of 128 x 128 split 2 ways;
-    # M = 16: the input gradient's 16 big tiles (4096 output columns) split 16
-    # ways over the 224 steps of its 14336-long reduction
-    assert L.stm_nf4_gemm_workspace_bytes(33, 14336, 4096, 0) == 2 * 33 * 14336 * 4
+    # M = 33, W [14336, 4096]: the small-M forward's 56 blocks of 256 weight
+    # rows x 32 groups of 128 split 4 ways (224 work-groups, one round; the
+    # tile path would split 2 ways); M = 16: the input gradient's 16 big tiles
+    # (4096 output columns) split 16 ways over the 224 steps of its 14336-long
+    # reduction
+    assert L.stm_nf4_gemm_workspace_bytes(33, 14336, 4096, 0) == 4 * 33 * 14336 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 14336, 4096, 1) == 16 * 16 * 4096 * 4
     # forward with M <= 16 where the split-free small-M kernel applies (the rows
     # fit and it fills the GPU): no partials of its own, so the workspace is

@@ -290,10 +290,10 @@ def test_lora_step_forced_fused_module_step(cuda, lora_step, monkeypatch):
     assert_gemm_close(lin.lora_B.grad, Br.grad, torch.bfloat16, "dB")
 
 
-@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("M", [1, 16, 32, 64])
 def test_decode_size_forward_and_input_gradient_at_full_weight_size(cuda, lora_step, M):
     """Decode-sized rows on the full W [14336, 4096]: the weight-streaming
-    small-M forward (split-free up to 16 rows, ranges + reduce at 32) and
+    small-M forward (split-free up to 16 rows, ranges + reduce at 32 and 64) and
     input gradient (ranges of weight rows + reduce), each with its rank-16
     LoRA term at an init that makes the term as large as the base product;
     whole matrix and every fragment against fp32 on the oracle weight."""

@@ -3,7 +3,7 @@
 The library picks, per call, the 256 x 256 tile (register-weight kernels, or
 LDS-weight kernels for some split reductions), the 128 x 256 register-weight
 tile (unsplit) or the 128 x 128 LDS-weight tile, split or not, and for a
-forward of at most 32 rows a weight-streaming small-M kernel: the split-free one
+forward of at most 64 rows a weight-streaming small-M kernel: the split-free one
 (its work-group's waves split the reduction and add bias and the LoRA term
 themselves) where the rows fit and the launch fills the GPU, else the one whose
 reduction ranges the split-reduce kernel sums (adding bias and the LoRA term).
@@ -122,6 +122,11 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (24, 520, 576, 64, True, 16),      # 32-row variant, split, LoRA in the reduce
     (31, 200, 448, 64, True, 0),       # 32-row variant, blocks of 192 rows (second partial), K % 256 == 192
     (32, 4104, 4160, 64, False, 16),   # 32-row variant, uneven ranges
+    (33, 8, 64, 64, True, 0),          # 64-row variant (groups of 128): one half group, unsplit with bias
+    (48, 520, 576, 64, True, 16),      # 64-row variant, K % 128 == 64, LoRA in the reduce
+    (64, 264, 4160, 64, False, 16),    # 64-row variant at its row limit: 33 groups over uneven ranges
+    (40, 1000, 1536, 256, True, 0),    # 64-row variant, blocksize 256 (a group is half a block)
+    (56, 4104, 1024, 512, True, 32),   # 64-row variant, blocksize 512, last block of 256 rows partly outside
     (320, 520, 576, 64, True, 16),     # last 256-row tile: 64 rows (the 2-fragment short item)
     (384, 264, 640, 64, False, 0),     # last 256-row tile: 128 rows (the 4-fragment short item)
     (100, 256, 1024, 128, True, 16),   # one tile of 100 rows (4 fragments), blocksize 128
