@@ -111,7 +111,7 @@ int stm_nf4_dequantize_many(int count, const uint8_t* const* packed, const float
  *                  (small M) the reduction is split over several work-groups
  *                  whose fp32 partials go there and are summed (in a fixed
  *                  order) by a second kernel; NULL disables the split. For
- *                  M <= 32 a weight-streaming kernel runs instead of the tiles:
+ *                  M <= 64 a weight-streaming kernel runs instead of the tiles:
  *                  in one launch with no workspace where its split-free form
  *                  fits (M <= 16 and enough weight rows to fill the GPU), else
  *                  when it has this workspace (or needs none: one range and no
