@@ -806,8 +806,9 @@ def run_small_m(torch, args):
     """M = 16 rows on the 14336 x 4096 weight (decode-sized): fused forward (the
     split-free weight-streaming small-M kernel, one launch) and input gradient
     (the weight-streaming small-M input-gradient kernel over ranges of weight
-    rows, plus the split reduce), against dequantize + hipBLASLt; and
-    the fused forward of a single row (batch-1 decode)."""
+    rows, plus the split reduce), against dequantize + hipBLASLt; the fused
+    forward of a single row (batch-1 decode); and both at 64 rows (the 64-row
+    layouts of the two weight-streaming kernels, ranges + split reduce)."""
     from stratum_amd.functional import dequantize_4bit, nf4_gemm_bwd_dx, nf4_gemm_fwd
     dev = torch.device("cuda:0")
     N, K, M = 14336, 4096, 16
@@ -821,11 +822,19 @@ def run_small_m(torch, args):
     ub = graph_time_ms(torch, lambda: dy @ dequantize_4bit(p, st), 20)
     x1 = x[:1].contiguous()
     f1 = graph_time_ms(torch, lambda: nf4_gemm_fwd(x1, p, st.absmax, (N, K), 64), 20)
+    x64 = seeded(torch, (64, K), 43, 1.0, torch.bfloat16, dev)
+    dy64 = seeded(torch, (64, N), 44, 1.0, torch.bfloat16, dev)
+    f64 = graph_time_ms(torch, lambda: nf4_gemm_fwd(x64, p, st.absmax, (N, K), 64), 20)
+    b64 = graph_time_ms(torch, lambda: nf4_gemm_bwd_dx(dy64, p, st.absmax, (N, K), 64), 20)
+    uf64 = graph_time_ms(torch, lambda: x64 @ dequantize_4bit(p, st).t(), 20)
+    ub64 = graph_time_ms(torch, lambda: dy64 @ dequantize_4bit(p, st), 20)
     wbytes = N * K / 2 + 4 * N * K / 64
     return {"M": M, "fused_fwd_ms": round(f, 4), "fused_bwd_ms": round(b, 4), "unfused_fwd_ms": round(uf, 4),
             "unfused_bwd_ms": round(ub, 4), "fused_fwd_weight_gbs": round(wbytes / f / 1e6, 1),
             "fused_bwd_weight_gbs": round(wbytes / b / 1e6, 1),
             "fused_fwd_m1_ms": round(f1, 4), "fused_fwd_m1_weight_gbs": round(wbytes / f1 / 1e6, 1),
+            "m64": {"fused_fwd_ms": round(f64, 4), "fused_bwd_ms": round(b64, 4),
+                    "unfused_fwd_ms": round(uf64, 4), "unfused_bwd_ms": round(ub64, 4)},
             "timing": "device time: 20 launches captured in one HIP graph, replayed (the input gradient's "
                       "split reduce included)"}
 
