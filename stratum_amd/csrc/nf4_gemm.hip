@@ -2204,19 +2204,22 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
     // group j S + s of buffer b: items i = TW c + u (chunk c of tile t0 + u; k =
     // 128 c + 32 h + 0..31 on lane (r, h)); the table reads of item i + 1 go out
     // before item i's math
-    auto compute = [&](int j, int b) {
+    // activation rows at or past M (never copied) only reach output columns
+    // that are not stored, so they are read as they are; TAIL (the group that
+    // reaches past K) zeroes the activations and scales of lanes past K
+    auto compute = [&](int j, int b, auto tail_c) {
+        constexpr bool TAIL = decltype(tail_c)::value;
         const int grp = j * S + s;
-        if (grp >= ngroups) return;
         const int64_t kg = (int64_t)grp * GV_GK;
         uint4 qv[2 * TW], xv[2][4];
         float av[2 * TW];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const bool ok = kg + 128 * c + 32 * h < K;
+            const bool ok = !TAIL || kg + 128 * c + 32 * h < K;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint4 v = bx(b)[(s * XR + rx) * 32 + ((16 * c + 4 * h + q) ^ r)];
-                xv[c][q] = (ok && r < M) ? v : make_uint4(0, 0, 0, 0);
+                xv[c][q] = ok ? v : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
             for (int u = 0; u < TW; ++u) {
@@ -2255,7 +2258,12 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
     for (int j = 0; j < steps; ++j) {
         const int b = j & 1;
         if (j + 1 < steps) copy_step(j + 1, b ^ 1);
-        compute(j, b);
+        const int grp = j * S + s;
+        if ((int64_t)(grp + 1) * GV_GK > K) {
+            if (grp < ngroups) compute(j, b, std::true_type());
+        } else {
+            compute(j, b, std::false_type());
+        }
         wait_vmem();
         __syncthreads();  // step j + 1 landed; every wave is done with buffer b
     }
