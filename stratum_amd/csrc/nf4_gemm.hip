@@ -1960,9 +1960,11 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
         for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // one group: work items (chunk c, tile t) in order i = R c + t; the table
-    // reads of item i + 1 are issued before item i's products, conversions and
-    // MFMAs. TAIL (the group that reaches past K) zeroes the activations and
-    // the scale of lanes whose k is past K.
+    // reads of item i + 1 are written before item i's products, conversions and
+    // MFMAs, with no scheduling fence between items (the compiler's
+    // interleaving across items measured 2-10 % faster than fenced items).
+    // TAIL (the group that reaches past K) zeroes the activations and the
+    // scale of lanes whose k is past K.
     auto compute = [&](int buf, int grp, auto tail_c) {
         constexpr bool TAIL = decltype(tail_c)::value;
         uint4 xv[C::NCH][MB][4], qv[C::NCH * R];
@@ -2003,7 +2005,6 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
 #pragma unroll
         for (int i = 0; i < C::NCH * R; ++i) {
             if (i + 1 < C::NCH * R) issue(i + 1, p[(i + 1) & 1]);
-            sched_fence();
             const int c = i / R, t = i % R;
             const float a = av[i];
 #pragma unroll
@@ -2017,7 +2018,6 @@ __global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, 
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) acc[t][mb] = mfma16<Tr>(w, xv[c][mb][q], acc[t][mb]);
             }
-            sched_fence();
         }
     };
 
@@ -2202,8 +2202,8 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
         }
     };
     // group j S + s of buffer b: items i = TW c + u (chunk c of tile t0 + u; k =
-    // 128 c + 32 h + 0..31 on lane (r, h)); the table reads of item i + 1 go out
-    // before item i's math
+    // 128 c + 32 h + 0..31 on lane (r, h)); the table reads of item i + 1 are
+    // written before item i's math, unfenced as in k_gemv_fwd
     // activation rows at or past M (never copied) only reach output columns
     // that are not stored, so they are read as they are; TAIL (the group that
     // reaches past K) zeroes the activations and scales of lanes past K
@@ -2234,7 +2234,6 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < 2 * TW; ++i) {
             if (i + 1 < 2 * TW) issue(qv[i + 1], p[(i + 1) & 1]);
-            sched_fence();
             const int c = i / TW, u = i % TW;
             const float a = av[i];
 #pragma unroll
@@ -2247,7 +2246,6 @@ __global__ __launch_bounds__(512) void k_gemv_ks(GemmArgs g) {
                 w.w = Tr::pack2(opaque(pq[3].x * a), opaque(pq[3].y * a));
                 acc[u] = mfma16<Tr>(w, xv[c][q], acc[u]);
             }
-            sched_fence();
         }
     };
 
