@@ -1853,11 +1853,12 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 // Work-group shape: WAVES waves of 32 weight rows (two 16-row MFMA tiles)
 // each. MB = 1: 8 waves (256 rows); MB = 2: 6 waves (192 rows), so the
 // doubled activation buffers still fit beside the 64 KB level table (150 KB
-// of LDS); MB = 4: 8 waves over groups of 128 (132 KB).
-template <int MB>
+// of LDS), or 8 waves over groups of 128 (116 KB); MB = 4: 8 waves over
+// groups of 128 (132 KB).
+template <int MB, int GK_>
 struct GvCfg {
-    static constexpr int WAVES = MB == 2 ? 6 : 8, R = 2, RW = 32, ROWS = RW * WAVES, XR = 16 * MB;
-    static constexpr int GK = MB == 4 ? 128 : 256;       // reduction depth of a group
+    static constexpr int GK = GK_;                       // reduction depth of a group
+    static constexpr int WAVES = MB == 2 && GK == 256 ? 6 : 8, R = 2, RW = 32, ROWS = RW * WAVES, XR = 16 * MB;
     static constexpr int PW = GK / 32, PX = GK / 8;      // 16-byte pieces of a weight row, an activation row
     static constexpr int NCH = GK / 128, NFL = GK / 64;  // 128-deep chunks; absmax per row (blocksize >= 64)
     static constexpr int WSH = PW == 8 ? 1 : 2;          // weight slot swizzle: piece ^ ((row >> WSH) % PW)
@@ -1868,9 +1869,9 @@ struct GvCfg {
 };
 constexpr int GV_GK = 256;  // group depth of k_gemv_ks
 
-template <typename Tr, int MB>
-__global__ __launch_bounds__(64 * GvCfg<MB>::WAVES) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
-    using C = GvCfg<MB>;
+template <typename Tr, int MB, int GK>
+__global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
+    using C = GvCfg<MB, GK>;
     constexpr int R = C::R, WAVES = C::WAVES;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2668,66 +2669,91 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
 #define STM_GEMV_T_LAT 3.0  // fixed cost of a work-group (copy latency, level table), in groups
 #endif
 
-int gemv_rows_per_block(int64_t M) {
-    return M <= 16 ? GvCfg<1>::ROWS : M <= 32 ? GvCfg<2>::ROWS : GvCfg<4>::ROWS;
-}
-int gemv_group_depth(int64_t M) { return M <= 16 ? GvCfg<1>::GK : M <= 32 ? GvCfg<2>::GK : GvCfg<4>::GK; }
+// Small-M forward plan: layout (activation blocks MB, group depth) and
+// reduction ranges. Up to 16 rows (MB = 1, 256 weight rows per work-group,
+// groups of 256): the ranges minimising rounds x (fixed cost + groups per
+// range) + 6 groups for the reduce. Above, the estimate is a fit to forced
+// range counts over eleven weight shapes (N, K from 1024 to 28672) at three
+// row counts per layout, in µs: a launch term, a cost per round of
+// work-groups (one per CU) and per group and round, and with a split a reduce
+// term per launch, per MB of fp32 partials and per range. At 17-32 rows both
+// MB = 2 layouts are estimated and the faster taken: 192 weight rows over
+// groups of 256 (6 waves) wins at N <= 6144 with K >= 2048, 256 rows over
+// groups of 128 (8 waves) at larger N or short K (e.g. [28672,4096]
+// 37.7 -> 29.8 us, [3072,1024] 13.4 -> 10.4 us at M = 17).
+struct GemvFit {
+    double launch, round, group, split, per_mb, per_range;
+};
+constexpr GemvFit kGv2Deep{4.97, 1.23, 1.91, 1.76, 0.47, 0.079};   // MB = 2, groups of 256 (7 % rms)
+constexpr GemvFit kGv2Short{4.34, 1.09, 1.10, 2.91, 0.41, 0.072};  // MB = 2, groups of 128 (3 % rms)
+constexpr GemvFit kGv4{5.15, 0.86, 1.61, 2.87, 0.38, 0.077};       // MB = 4, groups of 128 (3 % rms)
 
-// Small-M forward: reduction ranges (in groups of 256, 128 above 32 rows)
-// that minimise the estimated time, one work-group per CU, plus the split
-// reduce when there is more than one range. Up to 32 rows: rounds x (fixed
-// cost + groups per range) + 6 groups for the reduce. Above 32 rows, a fit
-// to forced range counts over eleven weight shapes (N, K from 1024 to 28672)
-// at M = 33, 48 and 64, in µs (3 % rms): 0.86 per round + 1.61 per group of
-// 128 and round, and with a split 2.87 + 0.38 per MB of partials + 0.08 per
-// range (the groups are latency-bound: one in flight per work-group).
-int gemv_splits(int64_t M, int64_t N, int64_t K) {
-    const int64_t rows = gemv_rows_per_block(M), gk = gemv_group_depth(M);
+struct GemvPlan {
+    int mb = 1, gk = 256, rows = 256, splits = 1;
+    double est = 0.0;
+};
+
+GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit* fit, int64_t M, int64_t N, int64_t K) {
+    GemvPlan p;
+    p.mb = mb, p.gk = gk, p.rows = rows;
     const int64_t blocks = (N + rows - 1) / rows, groups = (K + gk - 1) / gk;
-    if (groups <= 1) return 1;
-    int best = 1;
     double best_t = 1e30;
-    for (int64_t sp = 1; sp <= groups && sp <= 64; ++sp) {
-        const int64_t gps = (groups + sp - 1) / sp, spe = (groups + gps - 1) / gps;
+    for (int64_t sp = 1; sp <= (groups > 1 ? groups : 1) && sp <= 64; ++sp) {
+        const int64_t gps = groups > 0 ? (groups + sp - 1) / sp : 0;
+        const int64_t spe = gps > 0 ? (groups + gps - 1) / gps : 1;
         const int64_t rounds = (blocks * spe + 255) / 256;
-        const double t =
-            gk == 256 ? (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0)
-                      : (double)rounds * (0.86 + 1.61 * (double)gps) +
-                            (spe > 1 ? 2.87 + 0.38e-6 * (double)(spe * M * N * 4) + 0.077 * (double)spe : 0.0);
-        if (t < best_t - 1e-9) best_t = t, best = (int)spe;
+        double t;
+        if (!fit)
+            t = (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0);
+        else
+            t = fit->launch + (double)rounds * (fit->round + fit->group * (double)gps) +
+                (spe > 1 ? fit->split + fit->per_mb * 1e-6 * (double)(spe * M * N * 4) +
+                               fit->per_range * (double)spe
+                         : 0.0);
+        if (t < best_t - 1e-9) best_t = t, p.splits = (int)spe;
     }
-    return best;
+    p.est = best_t;
+    return p;
+}
+
+GemvPlan gemv_plan(int64_t M, int64_t N, int64_t K) {
+    if (M <= 16) return gemv_ranges(1, 256, GvCfg<1, 256>::ROWS, nullptr, M, N, K);
+    if (M > 32) return gemv_ranges(4, 128, GvCfg<4, 128>::ROWS, &kGv4, M, N, K);
+    const GemvPlan deep = gemv_ranges(2, 256, GvCfg<2, 256>::ROWS, &kGv2Deep, M, N, K);
+    const GemvPlan shrt = gemv_ranges(2, 128, GvCfg<2, 128>::ROWS, &kGv2Short, M, N, K);
+    return shrt.est < deep.est ? shrt : deep;
 }
 
 bool use_gemv(int64_t M, int num_groups) { return num_groups == 1 && M > 0 && M <= STM_GEMV_MAX_M; }
 
-int launch_gemv_fwd(GemmArgs g, int dtype, hipStream_t stream) {
-    const int gk = gemv_group_depth(g.M);
-    const int ngroups = (int)((g.K + gk - 1) / gk);
-    const int gps = (ngroups + g.splits - 1) / g.splits;
+int launch_gemv_fwd(GemmArgs g, const GemvPlan& p, int dtype, hipStream_t stream) {
+    const int ngroups = (int)((g.K + p.gk - 1) / p.gk);
+    const int gps = (ngroups + p.splits - 1) / p.splits;
     const int splits = gps ? (ngroups + gps - 1) / gps : 1;  // every range non-empty (K = 0: one empty range)
     g.splits = splits;
-    const int rows = gemv_rows_per_block(g.M);
-    dim3 grid((unsigned)((g.N + rows - 1) / rows), (unsigned)splits);
-    if (g.M <= 16) {
-        dim3 block(64 * GvCfg<1>::WAVES);
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_fwd<BF16, 1>), grid, block, 0, stream, g, gps);
-        else
-            hipLaunchKernelGGL((k_gemv_fwd<F16, 1>), grid, block, 0, stream, g, gps);
-    } else if (g.M <= 32) {
-        dim3 block(64 * GvCfg<2>::WAVES);
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_fwd<BF16, 2>), grid, block, 0, stream, g, gps);
-        else
-            hipLaunchKernelGGL((k_gemv_fwd<F16, 2>), grid, block, 0, stream, g, gps);
-    } else {
-        dim3 block(64 * GvCfg<4>::WAVES);
-        if (dtype == STM_BF16)
-            hipLaunchKernelGGL((k_gemv_fwd<BF16, 4>), grid, block, 0, stream, g, gps);
-        else
-            hipLaunchKernelGGL((k_gemv_fwd<F16, 4>), grid, block, 0, stream, g, gps);
+    dim3 grid((unsigned)((g.N + p.rows - 1) / p.rows), (unsigned)splits);
+#define STM_GV_LAUNCH(MB, GK)                                                                    \
+    {                                                                                            \
+        static_assert(GvCfg<MB, GK>::ROWS > 0, "config");                                        \
+        if (p.rows != GvCfg<MB, GK>::ROWS) return set_error(STM_ERR_INVALID, "gemv plan rows"); \
+        dim3 block(64 * GvCfg<MB, GK>::WAVES);                                                   \
+        if (dtype == STM_BF16)                                                                   \
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, MB, GK>), grid, block, 0, stream, g, gps);      \
+        else                                                                                     \
+            hipLaunchKernelGGL((k_gemv_fwd<F16, MB, GK>), grid, block, 0, stream, g, gps);       \
     }
+    if (p.mb == 1 && p.gk == 256 && g.M <= 16)
+        STM_GV_LAUNCH(1, 256)
+    else if (p.mb == 2 && p.gk == 256 && g.M <= 32)
+        STM_GV_LAUNCH(2, 256)
+    else if (p.mb == 2 && p.gk == 128 && g.M <= 32)
+        STM_GV_LAUNCH(2, 128)
+    else if (p.mb == 4 && p.gk == 128 && g.M <= 64)
+        STM_GV_LAUNCH(4, 128)
+    else
+        return set_error(STM_ERR_INVALID, "gemm_fwd: small-M plan MB %d, groups of %d for %lld rows", p.mb, p.gk,
+                         (long long)g.M);
+#undef STM_GV_LAUNCH
     int rc = check_launch("gemm_fwd (small M)");
     if (rc != STM_OK || g.splits == 1) return rc;
     return launch_split_reduce(g, g.N, g.bias, dtype, stream, true);
@@ -3097,7 +3123,7 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
     // small M: room for either kernel (a pinned tile kind skips the small-M one)
     int64_t gemv_need = 0;
     if (!backward && use_gemv(M, num_groups) && !gemv_ks_tiles(M, N, K)) {
-        const int sp = gemv_splits(M, N, K);
+        const int sp = gemv_plan(M, N, K).splits;
         gemv_need = sp > 1 ? (int64_t)sp * M * N * (int64_t)sizeof(float) : 0;
     }
     if (backward && use_gemv_bwd(M, N, K, num_groups))  // partials even for one range (the reduce adds LoRA)
@@ -3177,11 +3203,8 @@ int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     if (!g.offsets && use_gemv(g.M, g.num_groups) && tile_override() < 0) {
         const int kt = gemv_ks_tiles(g.M, g.N, g.K);
         if (kt) return launch_gemv_ks(g, kt, dtype, stream);
-        const int sp = gemv_splits(g.M, g.N, g.K);
-        if (sp == 1 ? g.lora_rank == 0 : g.partial != nullptr) {
-            g.splits = sp;
-            return launch_gemv_fwd(g, dtype, stream);
-        }
+        const GemvPlan gp = gemv_plan(g.M, g.N, g.K);
+        if (gp.splits == 1 ? g.lora_rank == 0 : g.partial != nullptr) return launch_gemv_fwd(g, gp, dtype, stream);
     }
     const Plan p = plan(g.M, g.N, g.K, false, g.num_groups);
     g.splits = (g.partial && p.splits > 1) ? p.splits : 1;

@@ -186,9 +186,12 @@ def test_gemm_workspace_sizing(L):
     # (3 + groups per range) + 6 for the reduce): 16 blocks x 56 groups -> 14
     # ranges of 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 4096, 14336, 0) == 14 * 16 * 4096 * 4
-    # 17..32 rows: blocks of 192 weight rows: 75 blocks x 16 groups -> 3 ranges
-    # of 6 (225 work-groups, one round)
-    assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 3 * 17 * 14336 * 4
+    # 17..32 rows, the faster of two estimated layouts: here 256 weight rows
+    # over groups of 128 (56 blocks x 32 groups -> 4 ranges of 8, 224
+    # work-groups) beats 192 rows over groups of 256 (3 ranges of 6)
+    assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 4 * 17 * 14336 * 4
+    # ... and on W [4096, 4096] the 192-row layout's 8 ranges of 2 groups
+    assert L.stm_nf4_gemm_workspace_bytes(20, 4096, 4096, 0) == 8 * 20 * 4096 * 4
     # a short reduction: the small-M kernel runs one range (no workspace), the
     # tile path (pinned tile kinds) splits 2 ways at 8 steps per range
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4

@@ -118,10 +118,13 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (9, 8200, 1024, 256, True, 16),    # split, last block of 256 weight rows partly outside
     (7, 264, 384, 128, True, 0),       # K % 256 == 128: last group's second chunk empty
     (11, 520, 448, 64, False, 0),      # K % 256 == 192: last group's second chunk half empty
-    (17, 8, 64, 64, True, 0),          # 32-row variant: one half chunk, unsplit with bias
-    (24, 520, 576, 64, True, 16),      # 32-row variant, split, LoRA in the reduce
-    (31, 200, 448, 64, True, 0),       # 32-row variant, blocks of 192 rows (second partial), K % 256 == 192
-    (32, 4104, 4160, 64, False, 16),   # 32-row variant, uneven ranges
+    (17, 8, 64, 64, True, 0),          # 32-row variant (256-row blocks, groups of 128): half a group, unsplit, bias
+    (24, 520, 576, 64, True, 16),      # 32-row variant (256-row blocks): 5 ranges, LoRA in the reduce
+    (31, 200, 448, 64, True, 0),       # 32-row variant (256-row blocks): 4 ranges, K % 128 == 64
+    (32, 4104, 4160, 64, False, 16),   # 32-row variant (192-row blocks, groups of 256), uneven ranges
+    (20, 4096, 4096, 128, True, 16),   # 32-row variant, 192-row blocks: 8 ranges, blocksize 128, bias + LoRA
+    (28, 1000, 1536, 512, True, 0),    # 32-row variant, 192-row blocks, blocksize 512
+    (26, 6152, 2048, 256, False, 32),  # 32-row variant, 256-row blocks over groups of 128, blocksize 256
     (33, 8, 64, 64, True, 0),          # 64-row variant (groups of 128): one half group, unsplit with bias
     (48, 520, 576, 64, True, 16),      # 64-row variant, K % 128 == 64, LoRA in the reduce
     (64, 264, 4160, 64, False, 16),    # 64-row variant at its row limit: 33 groups over uneven ranges
