@@ -1832,7 +1832,8 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 // bound by dequantizing the streamed weight. A work-group owns 32 weight rows
 // per wave (two v_mfma_f32_16x16x32 tiles of weight rows x activation rows,
 // 16 MB activation rows; GvCfg) over one reduction range, walked in groups of
-// GK = 256 (128 above 32 rows, whose larger activation buffers must fit).
+// GK = 256 or 128 (always 128 above 32 rows, whose larger activation buffers
+// must fit; at 17-32 rows the host picks the layout).
 // Every operand reaches LDS through lane-contiguous global -> LDS copies
 // (whole 64- or 128-byte row pieces), double-buffered, one barrier per group:
 //  - packed weight: each wave copies its own 32 rows x GK / 2 bytes (PW
