@@ -2667,17 +2667,15 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
 #endif
 
 #ifndef STM_GEMV_T_LAT
-#define STM_GEMV_T_LAT 3.0  // fixed cost of a work-group (copy latency, level table), in groups
+#define STM_GEMV_T_LAT 3.0  // small-M input gradient: fixed cost of a work-group, in groups
 #endif
 
 // Small-M forward plan: layout (activation blocks MB, group depth) and
-// reduction ranges. Up to 16 rows (MB = 1, 256 weight rows per work-group,
-// groups of 256): the ranges minimising rounds x (fixed cost + groups per
-// range) + 6 groups for the reduce. Above, the estimate is a fit to forced
-// range counts over eleven weight shapes (N, K from 1024 to 28672) at three
-// row counts per layout, in µs: a launch term, a cost per round of
-// work-groups (one per CU) and per group and round, and with a split a reduce
-// term per launch, per MB of fp32 partials and per range. At 17-32 rows both
+// reduction ranges minimising an estimate fitted to forced range counts over
+// ten or eleven weight shapes (N, K from 1024 to 28672) at three row counts
+// per layout, in µs: a launch term, a cost per round of work-groups (one per
+// CU) and per group and round, and with a split a reduce term per launch, per
+// MB of fp32 partials and per range. At 17-32 rows both
 // MB = 2 layouts are estimated and the faster taken: 192 weight rows over
 // groups of 256 (6 waves) wins at N <= 6144 with K >= 2048, 256 rows over
 // groups of 128 (8 waves) at larger N or short K (e.g. [28672,4096]
@@ -2685,6 +2683,7 @@ int launch_split_reduce(const GemmArgs& g, int64_t cols, const void* bias, int d
 struct GemvFit {
     double launch, round, group, split, per_mb, per_range;
 };
+constexpr GemvFit kGv1{4.18, 0.85, 1.69, 2.32, 0.52, 0.132};       // MB = 1, groups of 256 (2 % rms)
 constexpr GemvFit kGv2Deep{4.97, 1.23, 1.91, 1.76, 0.47, 0.079};   // MB = 2, groups of 256 (7 % rms)
 constexpr GemvFit kGv2Short{4.34, 1.09, 1.10, 2.91, 0.41, 0.072};  // MB = 2, groups of 128 (3 % rms)
 constexpr GemvFit kGv4{5.15, 0.86, 1.61, 2.87, 0.38, 0.077};       // MB = 4, groups of 128 (3 % rms)
@@ -2694,7 +2693,7 @@ struct GemvPlan {
     double est = 0.0;
 };
 
-GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit* fit, int64_t M, int64_t N, int64_t K) {
+GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit& fit, int64_t M, int64_t N, int64_t K) {
     GemvPlan p;
     p.mb = mb, p.gk = gk, p.rows = rows;
     const int64_t blocks = (N + rows - 1) / rows, groups = (K + gk - 1) / gk;
@@ -2703,14 +2702,10 @@ GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit* fit, int64_t M, in
         const int64_t gps = groups > 0 ? (groups + sp - 1) / sp : 0;
         const int64_t spe = gps > 0 ? (groups + gps - 1) / gps : 1;
         const int64_t rounds = (blocks * spe + 255) / 256;
-        double t;
-        if (!fit)
-            t = (double)rounds * (STM_GEMV_T_LAT + (double)gps) + (spe > 1 ? 6.0 : 0.0);
-        else
-            t = fit->launch + (double)rounds * (fit->round + fit->group * (double)gps) +
-                (spe > 1 ? fit->split + fit->per_mb * 1e-6 * (double)(spe * M * N * 4) +
-                               fit->per_range * (double)spe
-                         : 0.0);
+        const double t = fit.launch + (double)rounds * (fit.round + fit.group * (double)gps) +
+                         (spe > 1 ? fit.split + fit.per_mb * 1e-6 * (double)(spe * M * N * 4) +
+                                        fit.per_range * (double)spe
+                                  : 0.0);
         if (t < best_t - 1e-9) best_t = t, p.splits = (int)spe;
     }
     p.est = best_t;
@@ -2718,10 +2713,10 @@ GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit* fit, int64_t M, in
 }
 
 GemvPlan gemv_plan(int64_t M, int64_t N, int64_t K) {
-    if (M <= 16) return gemv_ranges(1, 256, GvCfg<1, 256>::ROWS, nullptr, M, N, K);
-    if (M > 32) return gemv_ranges(4, 128, GvCfg<4, 128>::ROWS, &kGv4, M, N, K);
-    const GemvPlan deep = gemv_ranges(2, 256, GvCfg<2, 256>::ROWS, &kGv2Deep, M, N, K);
-    const GemvPlan shrt = gemv_ranges(2, 128, GvCfg<2, 128>::ROWS, &kGv2Short, M, N, K);
+    if (M <= 16) return gemv_ranges(1, 256, GvCfg<1, 256>::ROWS, kGv1, M, N, K);
+    if (M > 32) return gemv_ranges(4, 128, GvCfg<4, 128>::ROWS, kGv4, M, N, K);
+    const GemvPlan deep = gemv_ranges(2, 256, GvCfg<2, 256>::ROWS, kGv2Deep, M, N, K);
+    const GemvPlan shrt = gemv_ranges(2, 128, GvCfg<2, 128>::ROWS, kGv2Short, M, N, K);
     return shrt.est < deep.est ? shrt : deep;
 }
 

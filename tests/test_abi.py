@@ -182,19 +182,23 @@ def test_gemm_workspace_sizing(L):
     assert L.stm_nf4_gemm_workspace_bytes(1, 4096, 14336, 0) == 8 * 1 * 4096 * 4
     # 16 rows of W [4096, 14336] do not fit it (16 rows need 4 tiles per
     # work-group: 64 work-groups): the split small-M kernel's ranges (blocks of
-    # 256 weight rows, one per CU; groups of 256 along K; fewest rounds x
-    # (3 + groups per range) + 6 for the reduce): 16 blocks x 56 groups -> 14
-    # ranges of 4
+    # 256 weight rows, one per CU; groups of 256 along K; least estimated
+    # time): 16 blocks x 56 groups -> 14 ranges of 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 4096, 14336, 0) == 14 * 16 * 4096 * 4
+    # a short reduction over few blocks still splits: W [3072, 1024] at 16
+    # rows -> 12 blocks x 4 groups -> 4 ranges of 1
+    assert L.stm_nf4_gemm_workspace_bytes(16, 3072, 1024, 0) == 4 * 16 * 3072 * 4
     # 17..32 rows, the faster of two estimated layouts: here 256 weight rows
     # over groups of 128 (56 blocks x 32 groups -> 4 ranges of 8, 224
     # work-groups) beats 192 rows over groups of 256 (3 ranges of 6)
     assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 4 * 17 * 14336 * 4
     # ... and on W [4096, 4096] the 192-row layout's 8 ranges of 2 groups
     assert L.stm_nf4_gemm_workspace_bytes(20, 4096, 4096, 0) == 8 * 20 * 4096 * 4
-    # a short reduction: the small-M kernel runs one range (no workspace), the
-    # tile path (pinned tile kinds) splits 2 ways at 8 steps per range
-    assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 2 * 16 * 256 * 4
+    # one block of weight rows over 4 groups: the small-M kernel's 4 ranges of
+    # one group (estimated below one work-group walking all 4), which is more
+    # than the tile path's 2 (pinned tile kinds, 8 steps per range); one group:
+    # one range, no workspace
+    assert L.stm_nf4_gemm_workspace_bytes(16, 256, 1024, 0) == 4 * 16 * 256 * 4
     assert L.stm_nf4_gemm_workspace_bytes(16, 256, 256, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(0, 256, 4096, 0) == 0
     assert L.stm_nf4_gemm_workspace_bytes(-1, 256, 256, 0) < 0
