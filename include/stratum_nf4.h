@@ -248,7 +248,9 @@ int stm_swiglu_bwd(const void* grad_out, const void* gate_up, void* grad_gate_up
  * T and U are the rank-R tensors the fused GEMMs take as lora_x. stm_lora_dy
  * reads dY once for both U and dB. fp32 accumulation; the fp32 partial sums of
  * the column/row blocks go to the caller's workspace and are added in a fixed
- * order (deterministic), scaled and rounded once. R in {8, 16, 24, 32}; the
+ * order (deterministic), scaled and rounded once; stm_lora_down at M <= 64
+ * (decode sizes) is one launch that sums each row's products in a fixed order
+ * itself and leaves the workspace unused. R in {8, 16, 24, 32}; the
  * column count of the large operand (K or N) a multiple of 8; all operands
  * 16-byte aligned, row-major and contiguous; dtype STM_BF16 or STM_F16.
  * Workspace: stm_lora_workspace_bytes(rows, cols, R, op) bytes, 16-byte aligned,

@@ -366,6 +366,74 @@ __global__ __launch_bounds__(256) void k_lora_reduce(RedJob j0, RedJob j1, int r
     }
 }
 
+// T = scaling * X . A^T for at most kDownRowsMax rows (decode sizes): one
+// launch, one work-group per row, no workspace (the pass + reduce pair costs
+// two launches). Thread j takes the 8-element pieces k = 8 j + 2048 i of the
+// row and of every A row (16-byte loads), fp32 products summed per thread in k
+// order; the 256 partial vectors meet in LDS in a fixed tree order, and the
+// row's R values are scaled and rounded once.
+constexpr int64_t kDownRowsMax = 64;
+template <typename Tr, int R>
+__global__ __launch_bounds__(256) void k_lora_down_rows(const uint16_t* __restrict__ X,
+                                                        const uint16_t* __restrict__ A, uint16_t* __restrict__ T,
+                                                        int64_t K, float scaling) {
+    __shared__ float red[256][R + 1];  // odd row stride: the tree's reads spread over the banks
+    const int tid = threadIdx.x;
+    const int64_t m = blockIdx.x;
+    const uint16_t* x = X + m * K;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    auto unpack = [](const uint4& v, float (&f)[8]) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f[2 * e] = Tr::to_f32((uint16_t)(w[e] & 0xFFFFu));
+            f[2 * e + 1] = Tr::to_f32((uint16_t)(w[e] >> 16));
+        }
+    };
+    for (int64_t k = 8 * (int64_t)tid; k < K; k += 2048) {
+        float xf[8];
+        unpack(*reinterpret_cast<const uint4*>(x + k), xf);
+        uint4 av[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) av[r] = *reinterpret_cast<const uint4*>(A + (int64_t)r * K + k);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float af[8];
+            unpack(av[r], af);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r] += xf[e] * af[e];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[tid][r] = acc[r];
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (tid < h) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[tid][r] += red[tid + h][r];
+        }
+        __syncthreads();
+    }
+    if (tid < R) T[m * R + tid] = Tr::from_f32(red[0][tid] * scaling);
+}
+
+template <typename Tr>
+void launch_down_rows(const void* X, const void* A, void* T, int64_t M, int64_t K, int R, float scaling,
+                      hipStream_t st) {
+    const dim3 grid((unsigned)M), block(256);
+    const auto* x = (const uint16_t*)X;
+    const auto* a = (const uint16_t*)A;
+    auto* t = (uint16_t*)T;
+    switch (R) {
+        case 8: hipLaunchKernelGGL((k_lora_down_rows<Tr, 8>), grid, block, 0, st, x, a, t, K, scaling); break;
+        case 16: hipLaunchKernelGGL((k_lora_down_rows<Tr, 16>), grid, block, 0, st, x, a, t, K, scaling); break;
+        case 24: hipLaunchKernelGGL((k_lora_down_rows<Tr, 24>), grid, block, 0, st, x, a, t, K, scaling); break;
+        default: hipLaunchKernelGGL((k_lora_down_rows<Tr, 32>), grid, block, 0, st, x, a, t, K, scaling); break;
+    }
+}
+
 int rank_padded(int R) { return R <= 16 ? 16 : 32; }
 
 // Blocks over the rows: about two work-groups per CU of MI355X's 256 in total,
@@ -513,6 +581,13 @@ extern "C" int stm_lora_down(const void* X, const void* A, void* T, int64_t M, i
     if (K == 0) {
         // no reduction: T = 0 (the reduce sums zero blocks)
         launch_reduce(part, 0, M, rank, 0.f, T, false, dtype, st);
+        return check_launch("lora_down");
+    }
+    if (M <= kDownRowsMax) {  // decode sizes: one launch, the workspace unused
+        if (dtype == STM_BF16)
+            launch_down_rows<BF16>(X, A, T, M, K, rank, scaling, st);
+        else
+            launch_down_rows<F16>(X, A, T, M, K, rank, scaling, st);
         return check_launch("lora_down");
     }
     LoraArgs a{(const uint16_t*)X, (const uint16_t*)A, nullptr, part, nullptr, M, K, rank, 1, (int)p.rpb};

@@ -17,6 +17,8 @@ SHAPES = [
     (130, 4104, 32),   # rank 32, 17 column blocks
     (2000, 4096, 16),  # several row blocks
     (513, 1000, 8),    # ragged in both directions
+    (16, 4104, 32),    # decode size: lora_down's one-launch kernel, 8 columns past a 2048 sweep
+    (40, 14336, 24),   # decode size, rank 24, long rows
 ]
 
 
