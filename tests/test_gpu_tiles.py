@@ -125,6 +125,8 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (20, 4096, 4096, 128, True, 16),   # 32-row variant, 192-row blocks: 8 ranges, blocksize 128, bias + LoRA
     (28, 1000, 1536, 512, True, 0),    # 32-row variant, 192-row blocks, blocksize 512
     (26, 6152, 2048, 256, False, 32),  # 32-row variant, 256-row blocks over groups of 128, blocksize 256
+    (22, 12296, 1024, 128, True, 16),  # 32-row variant, 256-row blocks: 4 ranges, blocksize 128, last block of 8 rows
+    (48, 8200, 1024, 128, False, 16),  # 64-row variant, blocksize 128, 4 ranges, last block of 8 rows
     (33, 8, 64, 64, True, 0),          # 64-row variant (groups of 128): one half group, unsplit with bias
     (48, 520, 576, 64, True, 16),      # 64-row variant, K % 128 == 64, LoRA in the reduce
     (64, 264, 4160, 64, False, 16),    # 64-row variant at its row limit: 33 groups over uneven ranges
