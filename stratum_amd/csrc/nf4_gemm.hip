@@ -1870,7 +1870,7 @@ struct GvCfg {
 };
 constexpr int GV_GK = 256;  // group depth of k_gemv_ks
 
-template <typename Tr, int MB, int GK>
+template <typename Tr, int MB, int GK, bool GROUPED = false>
 __global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmArgs g, int groups_per_split) {
     using C = GvCfg<MB, GK>;
     constexpr int R = C::R, WAVES = C::WAVES;
@@ -1888,12 +1888,31 @@ __global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmAr
         return reinterpret_cast<float*>(smem + C::kLut + 2 * (C::kX + C::kW) + buf * C::kA) + wave * (C::RW * C::NFL);
     };
 
-    const int64_t K = g.K, N = g.N, M = g.M;
+    const int64_t K = g.K, N = g.N;
     const int bshift = 31 - __builtin_clz(g.blocksize);
     const int nfl = (C::GK >> bshift) > 0 ? (C::GK >> bshift) : 1;  // absmax per row per group
     const int64_t kblocks = K >> bshift;
     const int ngroups = (int)((K + C::GK - 1) / C::GK);
-    const int z = blockIdx.y;
+    // GROUPED: expert blockIdx.y (one reduction range): its rows from the
+    // offsets, at most g.M (the caller's bound, at most 16 MB rows), its
+    // weight and its output rows; a work-group of an empty expert leaves
+    // before any barrier
+    int64_t M = g.M;
+    const uint16_t* xa = reinterpret_cast<const uint16_t*>(g.a);
+    const uint8_t* wpk = g.packed;
+    const float* wab = g.absmax;
+    uint16_t* yo = reinterpret_cast<uint16_t*>(g.out);
+    int z = blockIdx.y;
+    if constexpr (GROUPED) {
+        const Group gr = group_of(g, (int)blockIdx.y);
+        M = gr.rows < 0 ? 0 : gr.rows < g.M ? gr.rows : g.M;
+        if (M <= 0) return;
+        xa += gr.row0 * K;
+        yo += gr.row0 * N;
+        wpk = gr.packed;
+        wab = gr.absmax;
+        z = 0;
+    }
     const int g_begin = z * groups_per_split;
     const int g_end = g_begin + groups_per_split < ngroups ? g_begin + groups_per_split : ngroups;
     const int64_t nw0 = (int64_t)blockIdx.x * C::ROWS + wave * C::RW;  // this wave's first weight row
@@ -1907,14 +1926,14 @@ __global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmAr
     for (int i = 0; i < WC; ++i) {
         const int row = 64 / PW * i + lane / PW;
         const int64_t n = nw0 + row < N ? nw0 + row : N - 1;
-        wsrc[i] = g.packed + n * (K / 2) + 16 * wslot_piece(row, lane % PW);
+        wsrc[i] = wpk + n * (K / 2) + 16 * wslot_piece(row, lane % PW);
     }
     const int a_rows_per_copy = 64 / nfl, a_copies = (C::RW * nfl + 63) / 64;  // <= R
     const float* asrc[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int64_t n0 = nw0 + lane / nfl + i * a_rows_per_copy;
-        asrc[i] = g.absmax + (n0 < N ? n0 : N - 1) * kblocks;
+        asrc[i] = wab + (n0 < N ? n0 : N - 1) * kblocks;
     }
     const int aj = lane % nfl;
     // activations: XR PX / 64 copies of 64 / PX rows each, copy ix by wave ix % WAVES
@@ -1924,7 +1943,7 @@ __global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmAr
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
         const int xm = 64 / PX * (wave + j * WAVES) + lane / PX;  // activation row this lane copies
-        xsrc[j] = reinterpret_cast<const uint16_t*>(g.a) + (xm < M ? xm : M - 1) * K;
+        xsrc[j] = xa + (xm < M ? xm : M - 1) * K;
         xpiece[j] = (lane % PX) ^ (xm & 15);
     }
 
@@ -2062,7 +2081,7 @@ __global__ __launch_bounds__((64 * GvCfg<MB, GK>::WAVES)) void k_gemv_fwd(GemmAr
                 uint2 pk;
                 pk.x = Tr::pack2(v[0], v[1]);
                 pk.y = Tr::pack2(v[2], v[3]);
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + m * N + nc) = pk;
+                *reinterpret_cast<uint2*>(yo + m * N + nc) = pk;
             }
         }
 }
@@ -3200,8 +3219,47 @@ int launch_gemv_ks(const GemmArgs& g, int cfg, int dtype, hipStream_t stream) {
     return check_launch("gemm_fwd (small M, one launch)");
 }
 
+// 1: grouped forwards whose experts hold at most 64 rows run the
+// weight-streaming kernel.
+#ifndef STM_GEMV_GROUPED
+#define STM_GEMV_GROUPED 1
+#endif
+
+// Grouped forward with at most 64 rows per expert (the caller's max_rows, so
+// decode-sized MoE batches): one work-group per (block of weight rows,
+// expert), each over the whole reduction (no partials, no workspace); an
+// empty expert's work-groups leave at once. The tile path would run 192- or
+// 256-row tiles of MFMAs for each expert's few rows.
+int launch_gemv_grouped(GemmArgs g, int dtype, hipStream_t stream) {
+    g.splits = 1;
+#define STM_GG_LAUNCH(MB, GKV)                                                                          \
+    {                                                                                                   \
+        const int ng = (int)((g.K + GKV - 1) / GKV);                                                    \
+        const dim3 grid((unsigned)((g.N + GvCfg<MB, GKV>::ROWS - 1) / GvCfg<MB, GKV>::ROWS),            \
+                        (unsigned)g.num_groups),                                                        \
+            block(64 * GvCfg<MB, GKV>::WAVES);                                                          \
+        if (dtype == STM_BF16)                                                                          \
+            hipLaunchKernelGGL((k_gemv_fwd<BF16, MB, GKV, true>), grid, block, 0, stream, g, ng);      \
+        else                                                                                            \
+            hipLaunchKernelGGL((k_gemv_fwd<F16, MB, GKV, true>), grid, block, 0, stream, g, ng);       \
+    }
+    if (g.M <= 16)
+        STM_GG_LAUNCH(1, 256)
+    else if (g.M <= 32)
+        STM_GG_LAUNCH(2, 128)
+    else if (g.M <= 64)
+        STM_GG_LAUNCH(4, 128)
+    else
+        return set_error(STM_ERR_INVALID, "grouped gemm_fwd (small M): %lld rows per expert", (long long)g.M);
+#undef STM_GG_LAUNCH
+    return check_launch("grouped gemm_fwd (small M)");
+}
+
 int launch_gemm_fwd(const GemmArgs& g0, int dtype, hipStream_t stream) {
     GemmArgs g = g0;
+    if (g.offsets && STM_GEMV_GROUPED && g.M >= 1 && g.M <= STM_GEMV_MAX_M && g.num_groups <= 65535 && !g.bias &&
+        g.lora_rank == 0 && tile_override() < 0)
+        return launch_gemv_grouped(g, dtype, stream);
     // small M: the weight-streaming kernel, when its partials have a workspace
     // (or it needs none) and the LoRA term can go to the reduce; not for a
     // grouped call (its rows come from the offsets, even with one expert)

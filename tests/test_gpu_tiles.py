@@ -226,10 +226,10 @@ def test_input_gradient_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, rank
 @pytest.mark.parametrize("backward", [False, True])
 def test_grouped_call_with_one_expert_writes_only_its_rows(cuda, backward):
     """A grouped call with one expert of 5 rows and max_rows 16 (a bound, not
-    the row count) runs a grouped kernel, which takes its rows from the offsets:
-    the output rows past offsets[1] keep their contents, and the 5 rows match
-    the fp32 reference. (The small-M kernels take their rows from M and are not
-    used for grouped calls.)"""
+    the row count) runs a grouped kernel (the forward: the grouped form of the
+    weight-streaming kernel; the input gradient: the tiles), which takes its
+    rows from the offsets: the output rows past offsets[1] keep their contents,
+    and the 5 rows match the fp32 reference."""
     from stratum_amd import _lib
     from stratum_amd.functional import _gemm_dtype
     L = _lib.lib()
@@ -249,6 +249,44 @@ def test_grouped_call_with_one_expert_writes_only_its_rows(cuda, backward):
     ref = a[:rows].float() @ (wq.to(cuda) if backward else wq.to(cuda).t().contiguous())
     assert rel(out[:rows], ref) <= TOL[dtype]
     assert bool((out[rows:] == 7.0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("counts,N,K,bs", [
+    ([1, 0, 1, 1, 0, 1, 1, 1], 520, 576, 64),        # decode: one row per expert, empty experts, K % 256 == 64
+    ([3, 16, 0, 7, 16, 1], 264, 1024, 128),          # up to 16 rows (one activation block), blocksize 128
+    ([17, 0, 24, 5, 20], 1000, 320, 64),             # 17-32 rows: 256-row blocks over groups of 128, K % 128 == 64
+    ([33, 64, 0, 2, 48, 40, 1], 264, 1536, 256),     # 33-64 rows, blocksize 256 (a group is half a block)
+    ([9] * 40, 136, 512, 512),                       # 40 experts, blocksize 512
+])
+def test_grouped_forward_small_rows_per_expert(cuda, monkeypatch, dtype, counts, N, K, bs):
+    """Grouped forwards with at most 64 rows per expert run the grouped form of
+    the weight-streaming small-M kernel (one work-group per block of weight rows
+    and expert, rows from the offsets): every expert's rows against fp32 on the
+    oracle weights, every output row written, and the tile path (pinned) on the
+    same call within rounding."""
+    from stratum_amd.functional import nf4_grouped_gemm
+    E = len(counts)
+    w = seeded((E, N, K), 81, 0.02, torch.float16)
+    bits = w.reshape(-1, K).contiguous().view(torch.int16).numpy().view(np.uint16)
+    rp, ra = C.quantize(bits, O.DT_F16, bs, "argmin")
+    deq = C.dequantize(rp, ra, E * N * K, bs, TAG[dtype]).view(np.int16).reshape(E, N, K)
+    wq = torch.from_numpy(deq).view(dtype).float().to(cuda)
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    Mt = int(off[-1])
+    q, a = torch.from_numpy(rp).to(cuda), torch.from_numpy(ra).to(cuda)
+    x = seeded((Mt, K), 82, 1.0, dtype).to(cuda)
+    set_tile(monkeypatch, None)
+    y = torch.full((Mt, N), float("nan"), dtype=dtype, device=cuda)
+    nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs, out=y)
+    assert not bool(torch.isnan(y).any())
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi > lo:
+            assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], e
+    set_tile(monkeypatch, "big")
+    yt = nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs)
+    assert rel(y, yt) <= TOL[dtype] / 4
 
 
 @pytest.mark.parametrize("tile", ["big", "big8", "mid", "small"])
