@@ -192,7 +192,10 @@ int stm_nf4_gemm_set_tile(int kind);
  *             pick the tile height (stm_nf4_grouped_tile_rows). The kernels
  *             index rows by the device array alone, which is NOT read on the
  *             host: without host_offsets the caller guarantees its contract.
- *   max_rows: an upper bound on offsets[e+1] - offsets[e] (sizes the launch grid)
+ *   max_rows: an upper bound on offsets[e+1] - offsets[e] (sizes the launch grid);
+ *             at most 64 (decode-sized MoE batches): the weight-streaming
+ *             kernel runs per (block of weight rows, expert) instead of the
+ *             tiles, no workspace
  *   constraints: as stm_nf4_gemm_fwd
  */
 int stm_nf4_grouped_gemm_fwd(const void* X, const uint8_t* packed, const float* absmax, const int32_t* offsets,
