@@ -685,7 +685,8 @@ def run_layer_stream(torch, args):
 def run_moe(torch, args):
     """Qwen3-30B-A3B-like expert bank: 128 experts, gate_up [1536, 2048] and
     down [2048, 768] in NF4; 8192 tokens, top-8 of softmax(N(0,1) logits).
-    Fused grouped GEMMs against dequantize + a per-expert matmul loop."""
+    Fused grouped GEMMs against dequantize + a per-expert matmul loop; and the
+    same layer at a decode size (16 tokens)."""
     from stratum_amd.functional import dequantize_4bit, nf4_grouped_gemm
     dev = torch.device("cuda:0")
     E, H, I, T, TOPK = 128, 2048, 768, 8192, 8
@@ -732,13 +733,41 @@ def run_moe(torch, args):
     lib_ms = event_time_ms(torch, library, 10)
     loop_ms = event_time_ms(torch, lambda: expert_loop(gu_w, dn_w), 10)
     flops = 2.0 * rows * (2 * I * H + H * I)
+
+    # decode size: the first 16 tokens' routing (at most a few rows per expert:
+    # the grouped weight-streaming kernel), against the tile path pinned
+    from stratum_amd import _lib
+    TD = 16
+    cd = torch.bincount(top.reshape(T, TOPK)[:TD].reshape(-1), minlength=E)
+    off_d = torch.zeros(E + 1, dtype=torch.int32)
+    off_d[1:] = torch.cumsum(cd.cpu(), 0).to(torch.int32)
+    rows_d, max_d = int(off_d[-1]), int(cd.max().item())
+    x_d, h_d = x[:rows_d].contiguous(), h[:rows_d].contiguous()
+    yg_d = torch.empty((rows_d, 2 * I), dtype=torch.bfloat16, device=dev)
+    yd_d = torch.empty((rows_d, H), dtype=torch.bfloat16, device=dev)
+
+    def layer_d():
+        nf4_grouped_gemm(x_d, gu_p, gu_s.absmax, off_d, (2 * I, H), 64, max_rows=max_d, out=yg_d)
+        nf4_grouped_gemm(h_d, dn_p, dn_s.absmax, off_d, (H, I), 64, max_rows=max_d, out=yd_d)
+
+    dec_ms = event_time_ms(torch, layer_d, 20)
+    _lib.lib().stm_nf4_gemm_set_tile(0)
+    try:
+        dec_tile_ms = event_time_ms(torch, layer_d, 20)
+    finally:
+        _lib.lib().stm_nf4_gemm_set_tile(-1)
     return {"experts": E, "tokens": T, "top_k": TOPK, "rows": rows, "max_rows_per_expert": max_rows,
             "layer_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1), "gflop_per_layer": round(flops / 1e9, 1),
             "dequantize_plus_expert_loop": {"layer_ms": round(lib_ms, 4), "tflops": round(flops / lib_ms / 1e9, 1),
                                             "what": "k_dequantize over both banks + one hipBLASLt matmul per "
                                                     "expert and projection"},
             "expert_loop_dense_only_ms": round(loop_ms, 4),
-            "fused_speedup": round(lib_ms / ms, 3)}
+            "fused_speedup": round(lib_ms / ms, 3),
+            "decode_16tok": {"rows": rows_d, "max_rows_per_expert": max_d, "layer_ms": round(dec_ms, 4),
+                             "tile_path_layer_ms": round(dec_tile_ms, 4),
+                             "what": "gate_up + down for the first 16 tokens' top-8 routing: the grouped "
+                                     "weight-streaming kernel (at most 64 rows per expert) against the 256-row "
+                                     "tiles pinned; eager launches, HIP events"}}
 
 
 def run_mlp(torch, args):
