@@ -3176,24 +3176,32 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool backward, int
 
 // Configuration of the split-free small-M forward (k_gemv_ks), encoded as
 // T | TW << 4 | XR << 8, or 0 when none applies: the activation rows must fit
-// (M <= XR) and the launch must keep three quarters of the CUs busy. Among the
-// fits, the least estimated time: rounds x (fixed cost + tile-groups per wave),
-// the fixed cost (level table, first copies) counted as one tile-group and a
-// tile-group of a one-tile wave as 1.25 (half the work between barriers).
+// (M <= XR) and the launch must keep three quarters of the CUs busy, or, when
+// no configuration does and the reduction is at most 16 groups (K <= 4096),
+// half of them. Among the fits, the least estimated time: rounds x (fixed cost
+// + tile-groups per wave), the fixed cost (level table, first copies) counted
+// as one tile-group and a tile-group of a one-tile wave as 1.25 (half the work
+// between barriers). At 128-191 work-groups against the split kernel
+// (event-timed, µs): K <= 4096 faster, e.g. [4096,4096] M = 8 12.2 -> 10.0,
+// [2048,4096] M = 1 10.8 -> 7.6, [8192,1024] M = 12 10.5 -> 7.6, [8192,4096]
+// M = 16 14.3 / 14.5; K >= 11008 slower ([4096,14336] M = 8 17.5 / 20.2).
 int gemv_ks_config(int64_t M, int64_t N, int64_t K) {
     if (!STM_GEMV_KS || M < 1 || M > 16) return 0;
     static const int cfgs[][3] = {{1, 1, 4}, {2, 1, 8}, {4, 1, 16}, {8, 1, 16}, {4, 2, 4}};
     const int64_t groups = (K + GV_GK - 1) / GV_GK, cus = device_cus();
     int best = 0;
-    double best_t = 1e30;
-    for (const auto& c : cfgs) {
-        const int T = c[0], TW = c[1], XR = c[2], S = 8 * TW / T;
-        if (M > XR) continue;
-        const int64_t blocks = (N + 16 * T - 1) / (16 * T);
-        if (blocks * 4 < cus * 3) continue;
-        const int64_t rounds = (blocks + cus - 1) / cus;
-        const double t = (double)rounds * (1.0 + (double)((groups + S - 1) / S) * TW * (TW == 1 ? 1.25 : 1.0));
-        if (t < best_t) best_t = t, best = T | TW << 4 | XR << 8;
+    for (int pass = 0; pass < 2 && !best; ++pass) {
+        if (pass == 1 && groups > 16) break;
+        double best_t = 1e30;
+        for (const auto& c : cfgs) {
+            const int T = c[0], TW = c[1], XR = c[2], S = 8 * TW / T;
+            if (M > XR) continue;
+            const int64_t blocks = (N + 16 * T - 1) / (16 * T);
+            if (pass == 0 ? blocks * 4 < cus * 3 : blocks * 2 < cus) continue;
+            const int64_t rounds = (blocks + cus - 1) / cus;
+            const double t = (double)rounds * (1.0 + (double)((groups + S - 1) / S) * TW * (TW == 1 ? 1.25 : 1.0));
+            if (t < best_t) best_t = t, best = T | TW << 4 | XR << 8;
+        }
     }
     return best;
 }

@@ -144,6 +144,8 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (13, 25600, 1024, 512, False, 0),  # T = 8: one slice, blocksize 512 (one scale per group)
     (2, 12288, 4096, 128, True, 16),   # T = 4, two tiles per wave, 4 slices; blocksize 128, bias + LoRA
     (4, 14336, 4160, 64, False, 0),    # two tiles per wave: 17 groups, the last step holds one
+    (8, 4096, 4096, 64, True, 16),     # T = 2 at 128 work-groups (half the CUs; K <= 4096), bias + LoRA
+    (1, 2048, 2048, 128, False, 0),    # T = 1 at 128 work-groups, blocksize 128
 ])
 def test_forward_every_kernel(cuda, monkeypatch, dtype, M, N, K, bs, bias, rank):
     from stratum_amd import _lib
