@@ -254,14 +254,15 @@ def test_grouped_call_with_one_expert_writes_only_its_rows(cuda, backward):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("counts,N,K,bs", [
-    ([1, 0, 1, 1, 0, 1, 1, 1], 520, 576, 64),        # decode: one row per expert, empty experts, K % 256 == 64
-    ([3, 16, 0, 7, 16, 1], 264, 1024, 128),          # up to 16 rows (one activation block), blocksize 128
-    ([17, 0, 24, 5, 20], 1000, 320, 64),             # 17-32 rows: 256-row blocks over groups of 128, K % 128 == 64
-    ([33, 64, 0, 2, 48, 40, 1], 264, 1536, 256),     # 33-64 rows, blocksize 256 (a group is half a block)
-    ([9] * 40, 136, 512, 512),                       # 40 experts, blocksize 512
+@pytest.mark.parametrize("counts,N,K,bs,max_rows", [
+    ([1, 0, 1, 1, 0, 1, 1, 1], 520, 576, 64, None),        # decode: one row per expert, empty experts, K % 256 == 64
+    ([3, 16, 0, 7, 16, 1], 264, 1024, 128, None),          # up to 16 rows (one activation block), blocksize 128
+    ([17, 0, 24, 5, 20], 1000, 320, 64, None),             # 17-32 rows: 256-row blocks over groups of 128, K % 128 == 64
+    ([33, 64, 0, 2, 48, 40, 1], 264, 1536, 256, None),     # 33-64 rows, blocksize 256 (a group is half a block)
+    ([9] * 40, 136, 512, 512, None),                       # 40 experts, blocksize 512
+    ([1, 0, 3, 2], 264, 576, 64, 64),                      # max_rows 64 (a bound) over 0-3 rows: the 64-row layout
 ])
-def test_grouped_forward_small_rows_per_expert(cuda, monkeypatch, dtype, counts, N, K, bs):
+def test_grouped_forward_small_rows_per_expert(cuda, monkeypatch, dtype, counts, N, K, bs, max_rows):
     """Grouped forwards with at most 64 rows per expert run the grouped form of
     the weight-streaming small-M kernel (one work-group per block of weight rows
     and expert, rows from the offsets): every expert's rows against fp32 on the
@@ -280,14 +281,14 @@ def test_grouped_forward_small_rows_per_expert(cuda, monkeypatch, dtype, counts,
     x = seeded((Mt, K), 82, 1.0, dtype).to(cuda)
     set_tile(monkeypatch, None)
     y = torch.full((Mt, N), float("nan"), dtype=dtype, device=cuda)
-    nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs, out=y)
+    nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs, max_rows=max_rows, out=y)
     assert not bool(torch.isnan(y).any())
     for e in range(E):
         lo, hi = int(off[e]), int(off[e + 1])
         if hi > lo:
             assert rel(y[lo:hi], x[lo:hi].float() @ wq[e].t().contiguous()) <= TOL[dtype], e
     set_tile(monkeypatch, "big")
-    yt = nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs)
+    yt = nf4_grouped_gemm(x, q, a, off.to(cuda), (N, K), bs, max_rows=max_rows)
     assert rel(y, yt) <= TOL[dtype] / 4
 
 
