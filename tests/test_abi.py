@@ -194,6 +194,15 @@ def test_gemm_workspace_sizing(L):
     assert L.stm_nf4_gemm_workspace_bytes(17, 14336, 4096, 0) == 4 * 17 * 14336 * 4
     # ... and on W [4096, 4096] the 192-row layout's 8 ranges of 2 groups
     assert L.stm_nf4_gemm_workspace_bytes(20, 4096, 4096, 0) == 8 * 20 * 4096 * 4
+    assert L.stm_nf4_gemm_workspace_bytes(24, 4096, 4096, 0) == 8 * 24 * 4096 * 4
+    # W [28672, 4096] at 17 rows: 112 blocks of 256 rows -> 2 ranges (224 work-groups)
+    assert L.stm_nf4_gemm_workspace_bytes(17, 28672, 4096, 0) == 2 * 17 * 28672 * 4
+    # 64 rows (groups of 128): W [4096, 4096] -> 16 blocks x 32 groups -> 11 ranges of 3
+    assert L.stm_nf4_gemm_workspace_bytes(64, 4096, 4096, 0) == 11 * 64 * 4096 * 4
+    # input gradient at 64 rows of W [1024, 4096]: 8 groups of 128 weight rows;
+    # counting the partials' bytes keeps it at 4 ranges (the rule without them
+    # took 8)
+    assert L.stm_nf4_gemm_workspace_bytes(64, 1024, 4096, 1) == 4 * 64 * 4096 * 4
     # one block of weight rows over 4 groups: the small-M kernel's 4 ranges of
     # one group (estimated below one work-group walking all 4), which is more
     # than the tile path's 2 (pinned tile kinds, 8 steps per range); one group:
