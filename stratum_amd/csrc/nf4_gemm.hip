@@ -1854,8 +1854,8 @@ __global__ __launch_bounds__(256) void k_gemm_bwd_rw(GemmArgs g) {
 // Work-group shape: WAVES waves of 32 weight rows (two 16-row MFMA tiles)
 // each. MB = 1: 8 waves (256 rows); MB = 2: 6 waves (192 rows), so the
 // doubled activation buffers still fit beside the 64 KB level table (150 KB
-// of LDS), or 8 waves over groups of 128 (116 KB); MB = 4: 8 waves over
-// groups of 128 (132 KB).
+// of LDS), or 8 waves over groups of 128 (116 KB); MB = 3 and 4 (33-48 and
+// 49-64 rows): 8 waves over groups of 128 (124 and 132 KB).
 template <int MB, int GK_>
 struct GvCfg {
     static constexpr int GK = GK_;                       // reduction depth of a group
@@ -2733,6 +2733,7 @@ GemvPlan gemv_ranges(int mb, int gk, int rows, const GemvFit& fit, int64_t M, in
 
 GemvPlan gemv_plan(int64_t M, int64_t N, int64_t K) {
     if (M <= 16) return gemv_ranges(1, 256, GvCfg<1, 256>::ROWS, kGv1, M, N, K);
+    if (M > 32 && M <= 48) return gemv_ranges(3, 128, GvCfg<3, 128>::ROWS, kGv4, M, N, K);
     if (M > 32) return gemv_ranges(4, 128, GvCfg<4, 128>::ROWS, kGv4, M, N, K);
     const GemvPlan deep = gemv_ranges(2, 256, GvCfg<2, 256>::ROWS, kGv2Deep, M, N, K);
     const GemvPlan shrt = gemv_ranges(2, 128, GvCfg<2, 128>::ROWS, kGv2Short, M, N, K);
@@ -2763,6 +2764,8 @@ int launch_gemv_fwd(GemmArgs g, const GemvPlan& p, int dtype, hipStream_t stream
         STM_GV_LAUNCH(2, 256)
     else if (p.mb == 2 && p.gk == 128 && g.M <= 32)
         STM_GV_LAUNCH(2, 128)
+    else if (p.mb == 3 && p.gk == 128 && g.M <= 48)
+        STM_GV_LAUNCH(3, 128)
     else if (p.mb == 4 && p.gk == 128 && g.M <= 64)
         STM_GV_LAUNCH(4, 128)
     else
@@ -3255,6 +3258,8 @@ int launch_gemv_grouped(GemmArgs g, int dtype, hipStream_t stream) {
         STM_GG_LAUNCH(1, 256)
     else if (g.M <= 32)
         STM_GG_LAUNCH(2, 128)
+    else if (g.M <= 48)
+        STM_GG_LAUNCH(3, 128)
     else if (g.M <= 64)
         STM_GG_LAUNCH(4, 128)
     else

@@ -126,7 +126,7 @@ def variants(L, M, N, K, backward, monkeypatch, dev):
     (28, 1000, 1536, 512, True, 0),    # 32-row variant, 192-row blocks, blocksize 512
     (26, 6152, 2048, 256, False, 32),  # 32-row variant, 256-row blocks over groups of 128, blocksize 256
     (22, 12296, 1024, 128, True, 16),  # 32-row variant, 256-row blocks: 4 ranges, blocksize 128, last block of 8 rows
-    (48, 8200, 1024, 128, False, 16),  # 64-row variant, blocksize 128, 4 ranges, last block of 8 rows
+    (48, 8200, 1024, 128, False, 16),  # 48-row variant, blocksize 128, 4 ranges, last block of 8 rows
     (33, 8, 64, 64, True, 0),          # 64-row variant (groups of 128): one half group, unsplit with bias
     (48, 520, 576, 64, True, 16),      # 64-row variant, K % 128 == 64, LoRA in the reduce
     (64, 264, 4160, 64, False, 16),    # 64-row variant at its row limit: 33 groups over uneven ranges
@@ -260,6 +260,7 @@ def test_grouped_call_with_one_expert_writes_only_its_rows(cuda, backward):
     ([17, 0, 24, 5, 20], 1000, 320, 64, None),             # 17-32 rows: 256-row blocks over groups of 128, K % 128 == 64
     ([33, 64, 0, 2, 48, 40, 1], 264, 1536, 256, None),     # 33-64 rows, blocksize 256 (a group is half a block)
     ([9] * 40, 136, 512, 512, None),                       # 40 experts, blocksize 512
+    ([40, 0, 33, 7], 264, 576, 64, None),                  # 33-48 rows: the 48-row layout
     ([1, 0, 3, 2], 264, 576, 64, 64),                      # max_rows 64 (a bound) over 0-3 rows: the 64-row layout
 ])
 def test_grouped_forward_small_rows_per_expert(cuda, monkeypatch, dtype, counts, N, K, bs, max_rows):
